@@ -1,0 +1,315 @@
+"""Benchmark of the MaxSim hot path on one MI355X.
+
+Headline workload (the north-star configuration):
+one contrastive training step -- score_contrastive_train over Nq=Nb=512
+queries/documents (Lq=32, Ld ~ U[128, 1024], dim=128, bf16, L2-normalised
+Gaussian embeddings, 1% duplicated document tokens), cross-entropy over the
+diagonal, backward to dQ and dD.  Inputs are resident in HBM before timing.
+
+Printed as ONE JSON line.  ``value`` is the step throughput in TFLOP/s
+(F = 2*D*Nq*Lq*T_d forward flops per step / step time); ``ms_per_step`` is the
+user-level step time (including the API's host-side offset validation).
+Kernel-level timings, the other configurations (C2 contrastive 64x64, C3
+padded rerank docs/s, C4 packed pairs) and the CPU baseline are extra fields.
+
+    python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--quick", action="store_true", help="headline workload only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Workload generators (device-resident, seeded)
+# ---------------------------------------------------------------------------
+def make_c5(torch, dev, seed=0, nq=512, nb=512, lq=32, dim=128, lo=128, hi=1024, dup=0.01):
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (nb,), generator=g)
+    total = int(lens.sum())
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    q = F.normalize(torch.randn(nq, lq, dim, generator=gd, device=dev), dim=-1)
+    d = F.normalize(torch.randn(total, dim, generator=gd, device=dev), dim=-1)
+    off = torch.zeros(nb + 1, dtype=torch.int64)
+    off[1:] = lens.cumsum(0)
+    if dup > 0:
+        # overwrite 1% of document tokens with a copy of an earlier token of
+        # the same document (exact ties; the lowest index must win)
+        ndup = int(total * dup)
+        doc = torch.randint(0, nb, (ndup,), generator=g)
+        start, ln = off[doc], lens[doc]
+        pos = (torch.rand(ndup, generator=g) * (ln - 1)).long() + 1
+        src = (torch.rand(ndup, generator=g) * pos).long()
+        d[(start + pos).to(dev)] = d[(start + src).to(dev)]
+    return (q.to(torch.bfloat16), d.to(torch.bfloat16), off.to(torch.int32).to(dev),
+            lens.tolist())
+
+
+def make_c3(torch, dev, seed=0, B=256, C=1000, lq=32, ld=300, dim=128):
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(seed)
+    dlen = torch.randint(32, ld + 1, (B, C), generator=g, dtype=torch.int32)
+    q = torch.empty(B, lq, dim, dtype=torch.float16, device=dev)
+    d = torch.empty(B, C, ld, dim, dtype=torch.float16, device=dev)
+    for b in range(B):  # chunk-seeded so any query subset is reproducible
+        gb = torch.Generator(device=dev).manual_seed(seed * 100003 + b)
+        q[b] = F.normalize(torch.randn(lq, dim, generator=gb, device=dev), dim=-1).half()
+        d[b] = F.normalize(torch.randn(C, ld, dim, generator=gb, device=dev), dim=-1).half()
+    qlen = torch.full((B,), lq, dtype=torch.int32, device=dev)
+    return q, d, qlen, dlen.to(dev)
+
+
+def make_c4(torch, dev, seed=0, nq=512, nd=8192, npairs=20000, dim=128):
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(seed)
+    ql = torch.randint(8, 65, (nq,), generator=g)
+    dl = torch.exp(torch.randn(nd, generator=g) * 0.6 + torch.log(torch.tensor(180.0)))
+    dl = dl.round().clamp(16, 2048).long()
+    qoff = torch.zeros(nq + 1, dtype=torch.int32)
+    qoff[1:] = ql.cumsum(0)
+    doff = torch.zeros(nd + 1, dtype=torch.int32)
+    doff[1:] = dl.cumsum(0)
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    q = F.normalize(torch.randn(int(ql.sum()), dim, generator=gd, device=dev), dim=-1)
+    d = F.normalize(torch.randn(int(dl.sum()), dim, generator=gd, device=dev), dim=-1)
+    qids = torch.randint(0, nq, (npairs,), generator=g, dtype=torch.int32)
+    dids = torch.randint(0, nd, (npairs,), generator=g, dtype=torch.int32)
+    dscore = torch.randn(npairs, generator=g)
+    return (q.bfloat16(), qoff.to(dev), d.bfloat16(), doff.to(dev), qids.to(dev),
+            dids.to(dev), int(ql.max()), dscore.to(dev), ql, dl, qids, dids)
+
+
+# ---------------------------------------------------------------------------
+# Timing helpers
+# ---------------------------------------------------------------------------
+def time_events(torch, fn, reps, warmup):
+    """Average ms per call with HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the contrastive batch would shard); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import torch.nn.functional as F
+
+    import maxsim_amd
+    from maxsim_amd._ops import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    K, W = args.steps, args.warmup
+    extra = {}
+
+    # ---------------- C5: headline contrastive training step ----------------
+    log("C5: generating inputs")
+    q, d, off, lens = make_c5(torch, dev)
+    nq, lq, dim = q.shape
+    nb = off.numel() - 1
+    total = d.shape[0]
+    flops_fwd = 2.0 * dim * nq * lq * total
+    target = torch.arange(nq, device=dev)
+
+    qg = q.clone().requires_grad_(True)
+    dg = d.clone().requires_grad_(True)
+
+    def step():
+        qg.grad = None
+        dg.grad = None
+        scores = maxsim_amd.score_contrastive_train(qg, dg, off)
+        loss = F.cross_entropy(scores, target)
+        loss.backward()
+        return loss
+
+    log(f"C5: warmup {W} steps (T_d={total})")
+    for _ in range(W):
+        step()
+    torch.cuda.synchronize()
+    log(f"C5: timing {K} steps")
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / K
+
+    # kernel-level (op calls, no Python validation)
+    ms_fwd = time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(q, d, off), K, 2)
+    scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    dscore = (torch.softmax(scores, dim=1) - torch.eye(nq, device=dev)) / nq
+    ms_bwd = time_events(torch, lambda: ops.maxsim_contrastive_backward(dscore, q, d, off, argmax), K, 2)
+    ms_fwd_scoreonly = time_events(torch, lambda: ops.maxsim_contrastive_forward(q, d, off), K, 2)
+    bytes_bwd = (4 * nq * nb * lq + 4 * nq * nb + 2 * dim * (nq * lq + total)
+                 + 4 * dim * (nq * lq + total))
+    fwd_tflops = flops_fwd / (ms_fwd * 1e-3) / 1e12
+    extra["c5"] = {
+        "T_d": total, "flops_fwd": flops_fwd,
+        "step_ms": round(ms_step, 4),
+        "fwd_ms": round(ms_fwd, 4), "fwd_tflops": round(fwd_tflops, 2),
+        "fwd_scoreonly_ms": round(ms_fwd_scoreonly, 4),
+        "bwd_ms": round(ms_bwd, 4), "bwd_bytes": bytes_bwd,
+        "bwd_gbps": round(bytes_bwd / (ms_bwd * 1e-3) / 1e9, 1),
+        "bwd_hbm_frac": round(bytes_bwd / (ms_bwd * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "kernel_step_ms": round(ms_fwd + ms_bwd, 4),
+    }
+    log(f"C5: step {ms_step:.3f} ms, fwd {ms_fwd:.3f} ms ({fwd_tflops:.1f} TFLOP/s), bwd {ms_bwd:.3f} ms")
+
+    if not args.quick:
+        # ---------------- C2: small contrastive step ----------------
+        log("C2: contrastive 64x64")
+        q2, d2, off2, _ = make_c5(torch, dev, seed=1, nq=64, nb=64, lo=64, hi=512, dup=0.0)
+        q2g, d2g = q2.clone().requires_grad_(True), d2.clone().requires_grad_(True)
+        t2 = torch.arange(64, device=dev)
+
+        def step2():
+            q2g.grad = None
+            d2g.grad = None
+            F.cross_entropy(maxsim_amd.score_contrastive_train(q2g, d2g, off2), t2).backward()
+
+        for _ in range(W):
+            step2()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(K):
+            step2()
+        torch.cuda.synchronize()
+        extra["c2"] = {"step_ms": round((time.perf_counter() - t0) * 1e3 / K, 4),
+                       "fwd_ms": round(time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(q2, d2, off2), K, 2), 4)}
+
+        # ---------------- C3: padded rerank docs/s ----------------
+        log("C3: padded rerank 256x1000 (19.7 GB fp16)")
+        q3, d3, ql3, dl3 = make_c3(torch, dev)
+        B, C, Ld = d3.shape[0], d3.shape[1], d3.shape[2]
+        qf = q3.reshape(B * 32, 128)
+        df = d3.reshape(B * C * Ld, 128)
+        dlf = dl3.reshape(-1)
+        ms3 = time_events(torch, lambda: ops.maxsim_padded_forward(qf, ql3, df, dlf, 32, Ld, C), max(3, K // 4), 1)
+        real_rows = int(dl3.sum())
+        bytes3 = 2 * 128 * (real_rows + B * 32) + 8 * B * C
+        t0 = time.perf_counter()
+        maxsim_amd.score_candidates_padded(q3, d3, ql3, dl3)
+        torch.cuda.synchronize()
+        api3 = (time.perf_counter() - t0) * 1e3
+        extra["c3"] = {"kernel_ms": round(ms3, 4), "docs_per_s": round(B * C / (ms3 * 1e-3), 1),
+                       "gbps": round(bytes3 / (ms3 * 1e-3) / 1e9, 1),
+                       "hbm_frac": round(bytes3 / (ms3 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                       "api_ms_single_call": round(api3, 3)}
+        log(f"C3: {ms3:.3f} ms -> {B * C / (ms3 * 1e-3):.3e} docs/s")
+        del q3, d3, qf, df
+        torch.cuda.empty_cache()
+
+        # ---------------- C4: packed pairs fwd + bwd ----------------
+        log("C4: packed 20k pairs")
+        (q4, qo4, d4, do4, qi4, di4, mql, g4, *_rest) = make_c4(torch, dev)
+        ms4f = time_events(torch, lambda: ops.maxsim_packed_forward_with_argmax(q4, qo4, d4, do4, qi4, di4, mql), K, 2)
+        _, am4 = ops.maxsim_packed_forward_with_argmax(q4, qo4, d4, do4, qi4, di4, mql)
+        ms4b = time_events(torch, lambda: ops.maxsim_packed_backward(g4, q4, qo4, d4, do4, qi4, di4, am4, mql), K, 2)
+        extra["c4"] = {"fwd_ms": round(ms4f, 4), "bwd_ms": round(ms4b, 4)}
+
+    # ---------------- CPU baseline (bounded sample of C5) ----------------
+    cpu = None
+    if not args.no_cpu:
+        from oracle import torch_baseline
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        nsample = 16
+        qc = q[:nsample].float().cpu()
+        dc, mask = torch_baseline.pad_documents(d.float().cpu(), lens)
+        rows = torch.arange(nsample)
+        log(f"CPU baseline: {nsample} of {nq} query rows x {nb} docs on {cores} threads")
+        torch_baseline.contrastive_step(qc, rows, dc, mask, nq)  # warmup
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            torch_baseline.contrastive_step(qc, rows, dc, mask, nq)
+            times.append(time.perf_counter() - t0)
+        t_sample = statistics.median(times)
+        cpu_tflops = (flops_fwd * nsample / nq) / t_sample / 1e12
+        cpu = {"value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+               "sample": f"C5 fwd+CE+bwd for {nsample}/{nq} query rows against all {nb} docs "
+                         f"(fp32 einsum+max, -inf masked padding to Ld_max), median of 3 after 1 warmup; "
+                         f"{t_sample:.3f} s per sample step; host CPU: {cpu_model()}",
+               "step_ms_extrapolated": round(t_sample * nq / nsample * 1e3, 1)}
+        log(f"CPU baseline: {t_sample:.3f} s per sample -> {cpu_tflops:.4f} TFLOP/s")
+
+    value = flops_fwd / (ms_step * 1e-3) / 1e12
+    out = {
+        "metric": "contrastive fwd+bwd ms & MFMA TFLOP/s; rerank docs/sec at Lq=32 Ld=300 d=128",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded L2-normalised Gaussian embeddings, 1% duplicated doc tokens)",
+        "config": {"workload": "C5 contrastive training step: Nq=Nb=512, Lq=32, Ld~U[128,1024], "
+                               "dim=128, fwd + CE(diagonal) + bwd",
+                   "Nq": nq, "Nb": nb, "Lq": lq, "dim": dim, "total_doc_tokens": total},
+        "roofline": {"bound": "mfma", "kernel": "contrastive_tiled_kernel (forward + argmax)",
+                     "achieved": round(fwd_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

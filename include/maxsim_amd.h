@@ -1,0 +1,167 @@
+/*
+ * maxsim_amd.h -- C ABI of the MI355X (gfx950) MaxSim engine.
+ *
+ *   score(q, d) = sum_i max_j <q_i, d_j>        (fp32 accumulate, fp32 out)
+ *
+ * One entry point per operator of the reference's torch extension
+ * (torch-ext/torch_binding.cpp:7-90, documented in torch-ext/torch_binding.h).
+ * Every entry point:
+ *   - takes raw DEVICE pointers, int64 sizes, a dtype tag and a HIP stream
+ *     (pass a hipStream_t cast to void*; NULL = the null stream);
+ *   - never allocates or frees memory and keeps no state between calls;
+ *   - is asynchronous on `stream` (no host synchronisation);
+ *   - returns MAXSIM_OK or an error code; maxsim_amd_last_error() then gives
+ *     a message (thread-local, valid until the next call on that thread).
+ *
+ * Layout conventions (all arrays contiguous, row-major):
+ *   embeddings : [rows, dim] of `dtype`; rows of one query / document are
+ *                consecutive.
+ *   offsets    : int32 CSR offsets, [n + 1], offsets[0] == 0.
+ *   ids        : int32.
+ *   argmax     : int32, one slot per (pair, query token); slots beyond a
+ *                pair's real query length are written as 0.
+ *   grads      : fp32, shaped like the embeddings they belong to; every
+ *                element is written (callers need not zero them).
+ *
+ * Semantics shared by all forward entry points (reference maxsim.cu:412-443,
+ * tests/test_nan_inf.py): documents are scanned in ascending token order with
+ * a strict `>` (first index wins ties); NaN similarities never win, so a
+ * query token whose similarities are all NaN contributes -inf and argmax 0.
+ * Pairs whose offsets / ids / lengths are invalid are not read; their score
+ * is NaN and their argmax slots are 0.
+ */
+#ifndef MAXSIM_AMD_H_
+#define MAXSIM_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MAXSIM_FLOAT32 = 0,
+  MAXSIM_FLOAT16 = 1,
+  MAXSIM_BFLOAT16 = 2
+} maxsim_dtype;
+
+enum {
+  MAXSIM_OK = 0,
+  MAXSIM_ERR_INVALID = 1,     /* bad argument (null pointer, negative size...) */
+  MAXSIM_ERR_UNSUPPORTED = 2, /* valid but outside what this build supports   */
+  MAXSIM_ERR_LAUNCH = 3       /* the HIP runtime rejected a launch            */
+};
+
+/* Largest embedding dimension the kernels accept. */
+#define MAXSIM_AMD_MAX_DIM 256
+
+int maxsim_amd_abi_version(void);
+const char* maxsim_amd_last_error(void);
+
+/* ---- Packed ragged pairs ------------------------------------------------ */
+
+/* Replaces op `maxsim_forward` (torch_binding.h:21-27, maxsim.cu:819-922).
+ * queries [total_q_tokens, dim], query_offsets [num_queries+1],
+ * documents [total_d_tokens, dim], document_offsets [num_documents+1],
+ * pair_query_ids / pair_document_ids [num_pairs] -> scores [num_pairs].
+ * max_q_len > 0 bounds every query segment length (longer pairs are invalid). */
+int maxsim_amd_forward(maxsim_dtype dtype, const void* queries,
+                       int64_t total_q_tokens, const int32_t* query_offsets,
+                       int64_t num_queries, const void* documents,
+                       int64_t total_d_tokens, const int32_t* document_offsets,
+                       int64_t num_documents, const int32_t* pair_query_ids,
+                       const int32_t* pair_document_ids, int64_t num_pairs,
+                       int64_t dim, int64_t max_q_len, float* scores,
+                       void* stream);
+
+/* Replaces op `maxsim_packed_forward_with_argmax` (torch_binding.h:101-108,
+ * maxsim.cu:2039-2108).  As above plus argmax [num_pairs, max_q_len]. */
+int maxsim_amd_packed_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
+    const int32_t* query_offsets, int64_t num_queries, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* pair_query_ids,
+    const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
+    int64_t max_q_len, float* scores, int32_t* argmax, void* stream);
+
+/* Replaces op `maxsim_packed_backward` (torch_binding.h:112-121,
+ * maxsim.cu:2201-2286).  dscore [num_pairs] fp32, argmax [num_pairs,
+ * max_q_len] -> dqueries [total_q_tokens, dim], ddocuments [total_d_tokens,
+ * dim], both fp32. */
+int maxsim_amd_packed_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    float* dqueries, float* ddocuments, void* stream);
+
+/* ---- Padded rerank ------------------------------------------------------ */
+
+/* Replaces op `maxsim_padded_forward` (torch_binding.h:46-53,
+ * maxsim.cu:924-1024).  queries [B*Lq_max, dim], query_lengths [B],
+ * documents [B*C*Ld_max, dim], doc_lengths [B*C]; pair (b, c) scores query b
+ * against document b*C + c -> scores [B*C]. */
+int maxsim_amd_padded_forward(maxsim_dtype dtype, const void* queries,
+                              const int32_t* query_lengths,
+                              const void* documents,
+                              const int32_t* doc_lengths, int64_t batch,
+                              int64_t num_candidates, int64_t Lq_max,
+                              int64_t Ld_max, int64_t dim, float* scores,
+                              void* stream);
+
+/* Replaces op `maxsim_padded_forward_with_argmax` (torch_binding.h:65-72,
+ * maxsim.cu:1036-1116).  Adds argmax [B*C, Lq_max]. */
+int maxsim_amd_padded_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, const int32_t* query_lengths,
+    const void* documents, const int32_t* doc_lengths, int64_t batch,
+    int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
+    float* scores, int32_t* argmax, void* stream);
+
+/* Replaces op `maxsim_padded_backward` (torch_binding.h:86-95,
+ * maxsim.cu:1124-1210).  dscore [B*C] -> dqueries [B*Lq_max, dim],
+ * ddocuments [B*C*Ld_max, dim] (padding rows get 0). */
+int maxsim_amd_padded_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    const void* documents, const int32_t* query_lengths,
+    const int32_t* doc_lengths, const int32_t* argmax, int64_t batch,
+    int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
+    float* dqueries, float* ddocuments, void* stream);
+
+/* ---- Contrastive (all pairs) -------------------------------------------- */
+
+/* Replaces op `maxsim_contrastive_forward` (torch_binding.h:133-135,
+ * maxsim.cu:1718-1779).  queries [Nq, Lq, dim], documents [total_d_tokens,
+ * dim], document_offsets [Nb+1] -> scores [Nq, Nb]. */
+int maxsim_amd_contrastive_forward(maxsim_dtype dtype, const void* queries,
+                                   int64_t num_queries, int64_t Lq,
+                                   const void* documents,
+                                   int64_t total_d_tokens,
+                                   const int32_t* document_offsets,
+                                   int64_t num_documents, int64_t dim,
+                                   float* scores, void* stream);
+
+/* Replaces op `maxsim_contrastive_forward_with_argmax` (torch_binding.h:
+ * 144-147, maxsim.cu:1650-1716).  Adds argmax [Nq, Nb, Lq]. */
+int maxsim_amd_contrastive_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, int64_t num_queries, int64_t Lq,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents, int64_t dim,
+    float* scores, int32_t* argmax, void* stream);
+
+/* Replaces op `maxsim_contrastive_backward` (torch_binding.h:160-165,
+ * maxsim.cu:1856-1920).  dscore [Nq, Nb], argmax [Nq, Nb, Lq] ->
+ * dqueries [Nq, Lq, dim], ddocuments [total_d_tokens, dim]. */
+int maxsim_amd_contrastive_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    int64_t num_queries, int64_t Lq, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* argmax, int64_t dim,
+    float* dqueries, float* ddocuments, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* MAXSIM_AMD_H_ */

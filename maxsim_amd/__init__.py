@@ -1,0 +1,503 @@
+"""MaxSim on AMD Instinct MI355X (gfx950): ``score(q, d) = sum_i max_j <q_i, d_j>``.
+
+Drop-in for the Python surface of the reference package
+(torch-ext/maxsim/__init__.py, ``__all__`` at :38-56):
+
+* :func:`score_candidates_padded` (+ ``_with_argmax``, ``_train``) -- padded
+  reranking of ``[B, K, Ld, D]`` candidates per query.
+* :func:`score_contrastive` (+ ``_with_argmax``, ``_train``) -- all-pairs
+  ``[Nq, Nb]`` scores against packed documents; in-batch contrastive training.
+* :func:`score_pairs_packed` (+ ``_with_argmax``, ``_train``) -- arbitrary
+  ``(query, document)`` pair lists over ragged packed inputs.
+
+Every function validates its inputs on the host with the reference's error
+types and messages, then calls an operator of :mod:`maxsim_amd._ops`, which
+runs hand-written HIP kernels (fused MFMA forward with an in-register
+max/argmax epilogue; argmax-driven gather/scatter backward).  Scores are fp32;
+gradients are fp32 (autograd casts them to the input dtype for ``.grad``).
+
+The pure-PyTorch ``*_reference`` functions of the reference package are
+exported too (:mod:`maxsim_amd.reference`) for benchmarks and comparisons;
+they are never used by the operators.
+"""
+
+from __future__ import annotations
+
+from typing import Tuple
+
+import numpy as np
+import torch
+
+from ._ops import ops
+from .reference import (
+    maxsim_reference,
+    maxsim_reference_with_argmax,
+    score_candidates_padded_backward_reference,
+    score_candidates_padded_reference,
+    score_candidates_padded_with_argmax_reference,
+    score_contrastive_backward_reference,
+    score_contrastive_reference,
+    score_contrastive_with_argmax_reference,
+    score_pairs_packed_backward_reference,
+    score_pairs_packed_reference,
+    score_pairs_packed_with_argmax_reference,
+)
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "score_pairs_packed",
+    "score_pairs_packed_with_argmax",
+    "score_pairs_packed_train",
+    "score_candidates_padded",
+    "score_candidates_padded_with_argmax",
+    "score_candidates_padded_train",
+    "score_contrastive",
+    "score_contrastive_with_argmax",
+    "score_contrastive_train",
+    "maxsim_reference",
+    "maxsim_reference_with_argmax",
+    "score_pairs_packed_reference",
+    "score_pairs_packed_with_argmax_reference",
+    "score_candidates_padded_reference",
+    "score_candidates_padded_with_argmax_reference",
+    "score_contrastive_reference",
+    "score_contrastive_with_argmax_reference",
+]
+
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+_INDEXES = (torch.int32, torch.int64)
+
+
+# ---------------------------------------------------------------------------
+# Validation helpers (reference __init__.py:59-223, 812-877).  Host work is
+# vectorised: each call copies its layout metadata to the host once and checks
+# it with numpy instead of per-element Python loops.
+# ---------------------------------------------------------------------------
+def _require_float(name: str, t: torch.Tensor) -> None:
+    if t.dtype not in _FLOATS:
+        raise TypeError(f"{name} must be float32, float16, or bfloat16; got {t.dtype}")
+
+
+def _require_index(name: str, t: torch.Tensor) -> None:
+    if t.dtype not in _INDEXES:
+        raise TypeError(f"{name} must be int32 or int64; got {t.dtype}")
+
+
+def _require_one_device(**tensors: torch.Tensor) -> None:
+    items = list(tensors.items())
+    first_name, first = items[0]
+    for name, t in items[1:]:
+        if t.device != first.device:
+            raise RuntimeError(
+                "all tensors must be on the same device; "
+                f"{first_name} is on {first.device} but {name} is on {t.device}"
+            )
+
+
+def _to_host(*tensors: torch.Tensor) -> list[np.ndarray]:
+    """One device->host copy for several small int tensors."""
+    flat = [t.detach().reshape(-1).to(torch.int64) for t in tensors]
+    sizes = [f.numel() for f in flat]
+    joined = torch.cat(flat).cpu().numpy() if flat else np.zeros(0, np.int64)
+    out, pos = [], 0
+    for n in sizes:
+        out.append(joined[pos:pos + n])
+        pos += n
+    return out
+
+
+def _check_lengths(values: np.ndarray, max_len: int, name: str) -> None:
+    if (values <= 0).any():
+        raise ValueError(f"{name} must contain values > 0")
+    if (values > max_len).any():
+        raise ValueError(f"{name} values must be <= padded length {max_len}")
+
+
+def _check_padded(queries, documents, query_lengths, doc_lengths):
+    if queries.dim() != 3:
+        raise ValueError(f"queries must be 3-D [B, Lq, D]; got shape {tuple(queries.shape)}")
+    if documents.dim() != 4:
+        raise ValueError(
+            f"documents must be 4-D [B, C, Ld, D]; got shape {tuple(documents.shape)}"
+        )
+    B, Lq, D = queries.shape
+    Bd, C, Ld, Dd = documents.shape
+    if B != Bd:
+        raise ValueError(f"batch dim mismatch: queries B={B} but documents B={Bd}")
+    if D != Dd:
+        raise ValueError(f"embedding dim mismatch: queries D={D} but documents D={Dd}")
+    if tuple(query_lengths.shape) != (B,):
+        raise ValueError(
+            f"query_lengths must have shape [B={B}]; got {tuple(query_lengths.shape)}"
+        )
+    if tuple(doc_lengths.shape) != (B, C):
+        raise ValueError(
+            f"doc_lengths must have shape [B={B}, C={C}]; got {tuple(doc_lengths.shape)}"
+        )
+    if queries.dtype != documents.dtype:
+        raise TypeError(
+            "queries and documents must have the same dtype; got "
+            f"{queries.dtype} vs {documents.dtype}"
+        )
+    _require_float("queries", queries)
+    _require_float("documents", documents)
+    _require_index("query_lengths", query_lengths)
+    _require_index("doc_lengths", doc_lengths)
+    _require_one_device(queries=queries, documents=documents,
+                        query_lengths=query_lengths, doc_lengths=doc_lengths)
+    qlen, dlen = _to_host(query_lengths, doc_lengths)
+    _check_lengths(qlen, Lq, "query_lengths")
+    _check_lengths(dlen, Ld, "doc_lengths")
+    return B, C, Lq, Ld, D
+
+
+def _check_pair_ids(pair_query_ids, pair_document_ids) -> None:
+    if pair_query_ids.shape != pair_document_ids.shape:
+        raise ValueError(
+            "pair_query_ids and pair_document_ids must have the same shape; got "
+            f"{tuple(pair_query_ids.shape)} vs {tuple(pair_document_ids.shape)}"
+        )
+    if pair_query_ids.dim() != 1:
+        raise ValueError(f"pair_query_ids must be 1-D; got shape {tuple(pair_query_ids.shape)}")
+
+
+def _check_csr(values: np.ndarray, total: int, name: str) -> int:
+    """Offsets must start at 0, end at ``total`` and have no empty segment.
+    Returns the longest segment (reference __init__.py:178-196)."""
+    if values.size < 2:
+        raise RuntimeError(f"{name} must have length >= 2")
+    if values[0] != 0:
+        raise RuntimeError(f"{name}[0] must equal 0, got {int(values[0])}")
+    if values[-1] != total:
+        raise RuntimeError(
+            f"{name}[-1] ({int(values[-1])}) must equal total token count ({total})"
+        )
+    seg = np.diff(values)
+    bad = np.flatnonzero(seg <= 0)
+    if bad.size:
+        raise RuntimeError(f"empty segment in {name} at index {int(bad[0])}")
+    return int(seg.max())
+
+
+def _check_ids(values: np.ndarray, upper: int, name: str) -> None:
+    bad = np.flatnonzero((values < 0) | (values >= upper))
+    if bad.size:
+        i = int(bad[0])
+        raise RuntimeError(f"{name}[{i}] = {int(values[i])} out of range [0, {upper})")
+
+
+def _packed_layout(queries, query_offsets, documents, document_offsets,
+                   pair_query_ids, pair_document_ids) -> int:
+    qoff, doff, qids, dids = _to_host(query_offsets, document_offsets,
+                                      pair_query_ids, pair_document_ids)
+    max_q = _check_csr(qoff, queries.shape[0], "query_offsets")
+    _check_csr(doff, documents.shape[0], "document_offsets")
+    _check_ids(qids, qoff.size - 1, "pair_query_ids")
+    _check_ids(dids, doff.size - 1, "pair_document_ids")
+    return max_q
+
+
+def _resolve_max_q_len(max_q_len, actual: int) -> int:
+    if max_q_len is None:
+        return actual
+    if max_q_len <= 0:
+        raise ValueError(f"max_q_len must be > 0; got {max_q_len}")
+    if max_q_len < actual:
+        raise ValueError(
+            f"max_q_len ({max_q_len}) must be >= actual max query segment length ({actual})"
+        )
+    return int(max_q_len)
+
+
+def _check_packed_common(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, *, argmax_wording: bool):
+    if queries.dim() != 2:
+        suffix = "" if argmax_wording else " [total_q_tokens, dim]"
+        raise ValueError(f"queries must be 2-D{suffix}; got shape {tuple(queries.shape)}")
+    if documents.dim() != 2:
+        suffix = "" if argmax_wording else " [total_d_tokens, dim]"
+        raise ValueError(f"documents must be 2-D{suffix}; got shape {tuple(documents.shape)}")
+    if queries.shape[1] != documents.shape[1]:
+        raise ValueError(
+            f"queries.dim ({queries.shape[1]}) and documents.dim ({documents.shape[1]}) "
+            "must match"
+        )
+    if queries.dtype != documents.dtype:
+        raise TypeError(
+            "queries and documents must have the same dtype; got "
+            f"{queries.dtype} vs {documents.dtype}"
+        )
+    _require_float("queries", queries)
+    _require_float("documents", documents)
+    _require_index("query_offsets", query_offsets)
+    _require_index("document_offsets", document_offsets)
+    _require_index("pair_query_ids", pair_query_ids)
+    _require_index("pair_document_ids", pair_document_ids)
+    _require_one_device(queries=queries, query_offsets=query_offsets,
+                        documents=documents, document_offsets=document_offsets,
+                        pair_query_ids=pair_query_ids,
+                        pair_document_ids=pair_document_ids)
+    _check_pair_ids(pair_query_ids, pair_document_ids)
+
+
+def _check_contrastive(queries, documents, document_offsets) -> None:
+    _require_float("queries", queries)
+    _require_float("documents", documents)
+    _require_index("document_offsets", document_offsets)
+    if queries.dtype != documents.dtype:
+        raise TypeError(
+            f"queries and documents must share dtype; got {queries.dtype} and {documents.dtype}"
+        )
+    if queries.dim() != 3:
+        raise ValueError(f"queries must be 3-D [Nq, Lq, D]; got shape {tuple(queries.shape)}")
+    if documents.dim() != 2:
+        raise ValueError(
+            "documents must be 2-D [total_d_tokens, D] (packed); got shape "
+            f"{tuple(documents.shape)}"
+        )
+    if document_offsets.dim() != 1:
+        raise ValueError(
+            f"document_offsets must be 1-D [Nb+1]; got shape {tuple(document_offsets.shape)}"
+        )
+    if queries.shape[2] != documents.shape[1]:
+        raise ValueError(
+            f"queries.D ({queries.shape[2]}) must match documents.D ({documents.shape[1]})"
+        )
+    if queries.shape[1] <= 0:
+        raise ValueError(f"Lq must be > 0; got {queries.shape[1]}")
+    if queries.shape[2] <= 0:
+        raise ValueError(f"dim must be > 0; got {queries.shape[2]}")
+    if document_offsets.numel() < 2:
+        raise ValueError(
+            "document_offsets must have length >= 2 (at least one doc); "
+            f"got {document_offsets.numel()}"
+        )
+    _require_one_device(queries=queries, documents=documents,
+                        document_offsets=document_offsets)
+    (offs,) = _to_host(document_offsets)
+    total = documents.shape[0]
+    if offs[0] != 0:
+        raise ValueError(
+            f"document_offsets[0] must equal 0 (CSR offset convention); got {int(offs[0])}"
+        )
+    if offs[-1] != total:
+        raise ValueError(
+            f"document_offsets[-1] ({int(offs[-1])}) must equal total doc tokens ({total}); "
+            "the packed documents tensor and the offsets must agree on the total length"
+        )
+    bad = np.flatnonzero(np.diff(offs) <= 0)
+    if bad.size:
+        i = int(bad[0])
+        raise ValueError(
+            "document_offsets must be strictly increasing; got "
+            f"document_offsets[{i + 1}] ({int(offs[i + 1])}) <= "
+            f"document_offsets[{i}] ({int(offs[i])})"
+        )
+
+
+# ---------------------------------------------------------------------------
+# Packed pairs
+# ---------------------------------------------------------------------------
+def score_pairs_packed(queries, query_offsets, documents, document_offsets,
+                       pair_query_ids, pair_document_ids, *, max_q_len=None) -> torch.Tensor:
+    """MaxSim scores for a packed ragged list of (query, document) pairs.
+
+    Args:
+        queries: ``[total_q_tokens, dim]`` fp32 / fp16 / bf16.
+        query_offsets: ``[num_queries + 1]`` int32/int64 CSR offsets (start at
+            0, end at ``total_q_tokens``, no empty segment).
+        documents: ``[total_d_tokens, dim]``, same dtype as ``queries``.
+        document_offsets: ``[num_documents + 1]``, same rules.
+        pair_query_ids / pair_document_ids: ``[num_pairs]`` ids.
+        max_q_len: optional bound on query segment length (checked).
+
+    Returns:
+        ``[num_pairs]`` fp32 scores.
+    """
+    _check_packed_common(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, argmax_wording=False)
+    mql = _resolve_max_q_len(max_q_len, _packed_layout(
+        queries, query_offsets, documents, document_offsets,
+        pair_query_ids, pair_document_ids))
+    return ops.maxsim_forward(
+        queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
+        document_offsets.contiguous(), pair_query_ids.contiguous(),
+        pair_document_ids.contiguous(), mql)
+
+
+def score_pairs_packed_with_argmax(queries, query_offsets, documents, document_offsets,
+                                   pair_query_ids, pair_document_ids, *,
+                                   max_q_len=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """As :func:`score_pairs_packed`, plus the winning document-token index per
+    query token: int32 ``[num_pairs, max_q_len]`` (0 beyond a pair's length)."""
+    _check_packed_common(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, argmax_wording=True)
+    mql = _resolve_max_q_len(max_q_len, _packed_layout(
+        queries, query_offsets, documents, document_offsets,
+        pair_query_ids, pair_document_ids))
+    return ops.maxsim_packed_forward_with_argmax(
+        queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
+        document_offsets.contiguous(), pair_query_ids.contiguous(),
+        pair_document_ids.contiguous(), mql)
+
+
+class _PackedFn(torch.autograd.Function):
+    """Packed forward+argmax / backward pair (reference __init__.py:414-454)."""
+
+    @staticmethod
+    def forward(ctx, queries, query_offsets, documents, document_offsets,
+                pair_query_ids, pair_document_ids, max_q_len):
+        q, d = queries.contiguous(), documents.contiguous()
+        qoff, doff = query_offsets.contiguous(), document_offsets.contiguous()
+        qids, dids = pair_query_ids.contiguous(), pair_document_ids.contiguous()
+        scores, argmax = ops.maxsim_packed_forward_with_argmax(
+            q, qoff, d, doff, qids, dids, int(max_q_len))
+        ctx.save_for_backward(q, qoff, d, doff, qids, dids, argmax)
+        ctx.max_q_len = int(max_q_len)
+        return scores
+
+    @staticmethod
+    def backward(ctx, dscore):
+        q, qoff, d, doff, qids, dids, argmax = ctx.saved_tensors
+        dq, dd = ops.maxsim_packed_backward(
+            dscore.contiguous().to(torch.float32), q, qoff, d, doff, qids, dids,
+            argmax, ctx.max_q_len)
+        return dq, None, dd, None, None, None, None
+
+
+def score_pairs_packed_train(queries, query_offsets, documents, document_offsets,
+                             pair_query_ids, pair_document_ids, *,
+                             max_q_len=None) -> torch.Tensor:
+    """Differentiable :func:`score_pairs_packed` (fp32 gradients)."""
+    _check_packed_common(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, argmax_wording=True)
+    mql = _resolve_max_q_len(max_q_len, _packed_layout(
+        queries, query_offsets, documents, document_offsets,
+        pair_query_ids, pair_document_ids))
+    return _PackedFn.apply(queries, query_offsets, documents, document_offsets,
+                           pair_query_ids, pair_document_ids, mql)
+
+
+# ---------------------------------------------------------------------------
+# Padded candidates
+# ---------------------------------------------------------------------------
+def _padded_flat(queries, documents, query_lengths, doc_lengths):
+    B, Lq, D = queries.shape
+    _, C, Ld, _ = documents.shape
+    return (
+        queries.reshape(B * Lq, D).contiguous(),
+        documents.reshape(B * C * Ld, D).contiguous(),
+        query_lengths.to(torch.int32).contiguous(),
+        doc_lengths.reshape(B * C).to(torch.int32).contiguous(),
+    )
+
+
+def score_candidates_padded(queries, documents, query_lengths, doc_lengths) -> torch.Tensor:
+    """MaxSim of each query against its own ``C`` padded candidates.
+
+    Args:
+        queries: ``[B, Lq, dim]``; documents: ``[B, C, Ld, dim]``;
+        query_lengths: ``[B]`` in ``(0, Lq]``; doc_lengths: ``[B, C]`` in ``(0, Ld]``.
+        Rows beyond the lengths are never read.
+
+    Returns:
+        ``[B, C]`` fp32 scores.
+    """
+    B, C, Lq, Ld, _ = _check_padded(queries, documents, query_lengths, doc_lengths)
+    q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
+    return ops.maxsim_padded_forward(q, ql, d, dl, int(Lq), int(Ld), int(C)).view(B, C)
+
+
+def score_candidates_padded_with_argmax(queries, documents, query_lengths,
+                                        doc_lengths) -> Tuple[torch.Tensor, torch.Tensor]:
+    """As :func:`score_candidates_padded`, plus int32 argmax ``[B, C, Lq]``
+    (first index wins ties; 0 beyond ``query_lengths[b]``)."""
+    B, C, Lq, Ld, _ = _check_padded(queries, documents, query_lengths, doc_lengths)
+    q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
+    s, a = ops.maxsim_padded_forward_with_argmax(q, ql, d, dl, int(Lq), int(Ld), int(C))
+    return s.view(B, C), a.view(B, C, Lq)
+
+
+class _PaddedFn(torch.autograd.Function):
+    """Padded forward+argmax / backward pair (reference __init__.py:716-771)."""
+
+    @staticmethod
+    def forward(ctx, queries, documents, query_lengths, doc_lengths):
+        B, Lq, D = queries.shape
+        _, C, Ld, _ = documents.shape
+        q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
+        scores, argmax = ops.maxsim_padded_forward_with_argmax(
+            q, ql, d, dl, int(Lq), int(Ld), int(C))
+        ctx.save_for_backward(q, d, ql, dl, argmax)
+        ctx.shapes = (B, C, Lq, Ld, D)
+        return scores.view(B, C)
+
+    @staticmethod
+    def backward(ctx, dscore):
+        B, C, Lq, Ld, D = ctx.shapes
+        q, d, ql, dl, argmax = ctx.saved_tensors
+        dq, dd = ops.maxsim_padded_backward(
+            dscore.reshape(B * C).contiguous().to(torch.float32), q, d, ql, dl,
+            argmax, int(Lq), int(Ld), int(C))
+        return dq.view(B, Lq, D), dd.view(B, C, Ld, D), None, None
+
+
+def score_candidates_padded_train(queries, documents, query_lengths,
+                                  doc_lengths) -> torch.Tensor:
+    """Differentiable :func:`score_candidates_padded` (fp32 gradients)."""
+    _check_padded(queries, documents, query_lengths, doc_lengths)
+    return _PaddedFn.apply(queries, documents, query_lengths, doc_lengths)
+
+
+# ---------------------------------------------------------------------------
+# Contrastive (all pairs)
+# ---------------------------------------------------------------------------
+def score_contrastive(queries, documents, document_offsets) -> torch.Tensor:
+    """Score every query against every packed document.
+
+    Args:
+        queries: ``[Nq, Lq, dim]``; documents: ``[total_d_tokens, dim]`` packed;
+        document_offsets: ``[Nb + 1]`` CSR offsets.
+
+    Returns:
+        ``[Nq, Nb]`` fp32 scores.
+    """
+    _check_contrastive(queries, documents, document_offsets)
+    return ops.maxsim_contrastive_forward(
+        queries.contiguous(), documents.contiguous(),
+        document_offsets.to(torch.int32).contiguous())
+
+
+def score_contrastive_with_argmax(queries, documents,
+                                  document_offsets) -> Tuple[torch.Tensor, torch.Tensor]:
+    """As :func:`score_contrastive`, plus int32 argmax ``[Nq, Nb, Lq]``."""
+    _check_contrastive(queries, documents, document_offsets)
+    return ops.maxsim_contrastive_forward_with_argmax(
+        queries.contiguous(), documents.contiguous(),
+        document_offsets.to(torch.int32).contiguous())
+
+
+class _ContrastiveFn(torch.autograd.Function):
+    """Contrastive forward+argmax / backward pair (reference __init__.py:925-954)."""
+
+    @staticmethod
+    def forward(ctx, queries, documents, document_offsets):
+        q, d = queries.contiguous(), documents.contiguous()
+        offs = document_offsets.to(torch.int32).contiguous()
+        scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, offs)
+        ctx.save_for_backward(q, d, offs, argmax)
+        return scores
+
+    @staticmethod
+    def backward(ctx, dscore):
+        q, d, offs, argmax = ctx.saved_tensors
+        dq, dd = ops.maxsim_contrastive_backward(
+            dscore.contiguous().to(torch.float32), q, d, offs, argmax)
+        return dq, dd, None
+
+
+def score_contrastive_train(queries, documents, document_offsets) -> torch.Tensor:
+    """Differentiable :func:`score_contrastive` (fp32 gradients)."""
+    _check_contrastive(queries, documents, document_offsets)
+    return _ContrastiveFn.apply(queries, documents, document_offsets)

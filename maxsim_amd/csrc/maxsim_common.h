@@ -1,0 +1,179 @@
+// Shared device code for the MaxSim kernels (gfx950 / CDNA4).
+//
+// Tile geometry used by every forward kernel
+// ------------------------------------------
+// One MFMA output tile is 32 document rows (M) x 32 query tokens (N), built
+// from K-chunks of 16 embedding elements:
+//   * bf16 / fp16 : one v_mfma_f32_32x32x16_{bf16,f16} per K-chunk
+//   * fp32        : eight v_mfma_f32_32x32x2_f32 per K-chunk
+// Lane l = c + 32*h (c = l & 31, h = l >> 5) supplies, for K-chunk s,
+//   A: document row  (tile_row0 + c), elements [16s + 8h, 16s + 8h + 8)
+//   B: query token   (tok0 + c),      elements [16s + 8h, 16s + 8h + 8)
+// Because A and B use the same (lane-half, element) -> k mapping, the MFMA
+// sums exactly the products q[k] * d[k] over the chunk.  The fp32 path maps
+// instruction e of the chunk to k = 16s + 8h + e, which is the same set.
+// Accumulator register r of lane l holds
+//   S[row = 8*(r>>2) + 4*h + (r&3)][col = c]
+// so each lane owns ONE query token and 16 document rows per tile, in
+// ascending row order.  The running max/argmax is therefore a per-lane
+// register update; the two lane halves are merged once per document.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace maxsim {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kTileRows = 32;   // document rows per MFMA tile
+constexpr int kTileCols = 32;   // query tokens per MFMA tile (one "query block")
+constexpr int kChunk = 16;      // embedding elements per K-chunk
+
+// Element tags (storage is raw bits; arithmetic happens inside MFMA).
+struct BF16 { typedef uint16_t storage; static constexpr int bytes = 2; };
+struct F16  { typedef uint16_t storage; static constexpr int bytes = 2; };
+struct F32  { typedef float    storage; static constexpr int bytes = 4; };
+
+// Per-lane operand fragment for one K-chunk: 8 elements.
+template <typename T> struct Frag;
+template <> struct Frag<BF16> { uint4 v; };
+template <> struct Frag<F16>  { uint4 v; };
+template <> struct Frag<F32>  { uint4 lo, hi; };
+
+template <typename T>
+__device__ __forceinline__ Frag<T> zero_frag() {
+  Frag<T> f;
+  if constexpr (T::bytes == 2) {
+    f.v = make_uint4(0, 0, 0, 0);
+  } else {
+    f.lo = make_uint4(0, 0, 0, 0);
+    f.hi = make_uint4(0, 0, 0, 0);
+  }
+  return f;
+}
+
+// Load 8 elements [k0, k0+8) of a row.  `vec` means the row pointer plus k0
+// is 16-byte aligned and k0 + 8 <= dim; otherwise elements at k >= dim read
+// as zero and the load is element-wise.
+template <typename T>
+__device__ __forceinline__ Frag<T> load_frag(const typename T::storage* row,
+                                             int k0, int dim, bool vec) {
+  Frag<T> f;
+  if (vec) {
+    if constexpr (T::bytes == 2) {
+      f.v = *reinterpret_cast<const uint4*>(row + k0);
+    } else {
+      f.lo = *reinterpret_cast<const uint4*>(row + k0);
+      f.hi = *reinterpret_cast<const uint4*>(row + k0 + 4);
+    }
+    return f;
+  }
+  if constexpr (T::bytes == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = k0 + 2 * e;
+      const uint32_t lo = (k < dim) ? (uint32_t)row[k] : 0u;
+      const uint32_t hi = (k + 1 < dim) ? (uint32_t)row[k + 1] : 0u;
+      w[e] = lo | (hi << 16);
+    }
+    f.v = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (k0 + e < dim) ? row[k0 + e] : 0.0f;
+    f.lo = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]),
+                      __float_as_uint(x[2]), __float_as_uint(x[3]));
+    f.hi = make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]),
+                      __float_as_uint(x[6]), __float_as_uint(x[7]));
+  }
+  return f;
+}
+
+// acc += A(32 rows x 16 k) * B(16 k x 32 tokens) for one K-chunk.
+__device__ __forceinline__ void mma_chunk(const Frag<BF16>& a,
+                                          const Frag<BF16>& b, f32x16& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+      __builtin_bit_cast(bf16x8, a.v), __builtin_bit_cast(bf16x8, b.v), acc,
+      0, 0, 0);
+}
+__device__ __forceinline__ void mma_chunk(const Frag<F16>& a,
+                                          const Frag<F16>& b, f32x16& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+      __builtin_bit_cast(f16x8, a.v), __builtin_bit_cast(f16x8, b.v), acc,
+      0, 0, 0);
+}
+__device__ __forceinline__ void mma_chunk(const Frag<F32>& a,
+                                          const Frag<F32>& b, f32x16& acc) {
+  const uint32_t av[8] = {a.lo.x, a.lo.y, a.lo.z, a.lo.w,
+                          a.hi.x, a.hi.y, a.hi.z, a.hi.w};
+  const uint32_t bv[8] = {b.lo.x, b.lo.y, b.lo.z, b.lo.w,
+                          b.hi.x, b.hi.y, b.hi.z, b.hi.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(
+        __uint_as_float(av[e]), __uint_as_float(bv[e]), acc, 0, 0, 0);
+}
+
+// Row (within the 32-row tile) held by accumulator register r of lane-half h.
+__device__ __forceinline__ constexpr int acc_row(int r, int h) {
+  return 8 * (r >> 2) + 4 * h + (r & 3);
+}
+
+// Rows at or beyond `valid` (only in a document's last, partial tile) must
+// never win: they were loaded from a clamped row and are forced to -inf.
+__device__ __forceinline__ void mask_rows(f32x16& acc, int h, int valid) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (acc_row(r, h) >= valid) acc[r] = -__builtin_inff();
+}
+
+// Running max / argmax update for one tile.  Semantics (shared with the
+// reference kernels, maxsim.cu:412-443): ascending document order, strict
+// `>` so the first index wins ties, NaN never wins (fmaxf ignores NaN and
+// `>`/`==` are false for NaN).  `row_base` is tile_row0 + 4*h.
+template <bool ARGMAX>
+__device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
+                                            int& am, int row_base) {
+  const float t0 = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
+  const float t1 = fmaxf(fmaxf(acc[3], acc[4]), acc[5]);
+  const float t2 = fmaxf(fmaxf(acc[6], acc[7]), acc[8]);
+  const float t3 = fmaxf(fmaxf(acc[9], acc[10]), acc[11]);
+  const float t4 = fmaxf(fmaxf(acc[12], acc[13]), acc[14]);
+  const float t5 = fmaxf(fmaxf(t0, t1), t2);
+  const float t6 = fmaxf(fmaxf(t3, t4), acc[15]);
+  const float tmax = fmaxf(t5, t6);
+  if (tmax > m) {
+    m = tmax;
+    if constexpr (ARGMAX) {
+      int idx = 15;
+#pragma unroll
+      for (int r = 14; r >= 0; --r) idx = (acc[r] == tmax) ? r : idx;
+      am = row_base + 8 * (idx >> 2) + (idx & 3);
+    }
+  }
+}
+
+// Merge the two lane halves that own the same query token: larger value
+// wins, equal values keep the lower document index.
+__device__ __forceinline__ void merge_halves(float& m, int& am) {
+  const float mo = __shfl_xor(m, 32);
+  const int ao = __shfl_xor(am, 32);
+  if (mo > m || (mo == m && ao < am)) {
+    m = mo;
+    am = ao;
+  }
+}
+
+// Sum of `v` over the 32 lanes of each half (fixed butterfly order, so the
+// result is deterministic); every lane receives its half's sum.
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+}  // namespace maxsim

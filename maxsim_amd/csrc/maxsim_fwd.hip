@@ -1,0 +1,799 @@
+// MaxSim forward kernels for gfx950 and the forward C-ABI entry points.
+//
+// Two kernels share the tile math of maxsim_common.h:
+//
+//  * contrastive_tiled_kernel -- all-pairs scoring (reference K6/K7,
+//    maxsim.cu:1227-1595).  A workgroup of 8 waves holds up to 16 query
+//    blocks (32 tokens each) in registers and streams the 32-row tiles of a
+//    chunk of documents through double-buffered LDS, so each document tile is
+//    read from L2 once per 16 queries instead of once per pair.  The
+//    blockIdx -> (query group, doc chunk) map keeps all query groups of a doc
+//    chunk on one XCD so the chunk is fetched into that XCD's L2 once.
+//
+//  * pair_kernel -- one wave per run of (query, document) pairs, document
+//    rows loaded straight from global memory into MFMA operand registers
+//    (reference K1/K2/K3/K5/K9, maxsim.cu:70-322, 647-698, 1933-2010).  Used
+//    for padded rerank and packed pairs, whose document tiles are each used
+//    by a single query (HBM-bound), and for contrastive shapes the tiled
+//    kernel does not cover (Lq > 64).
+//
+// Neither kernel writes the [Lq, Ld] similarity matrix anywhere: each
+// 32x32 MFMA tile is reduced in registers (tile_update) and discarded.
+#include <string>
+#include <cstdio>
+#include <cstdarg>
+
+#include "maxsim_common.h"
+#include "maxsim_host.h"
+
+namespace maxsim {
+
+enum Mode : int { kContrastive = 0, kPadded = 1, kPacked = 2 };
+
+struct FwdArgs {
+  const void* q;
+  const void* d;
+  int dim;
+  int mode;
+  int64_t npairs;
+  int slots;  // argmax row stride (Lq for contrastive, Lq_max, max_q_len)
+  // contrastive
+  int64_t nb;
+  int lq;
+  const int32_t* doff;
+  int64_t total_d;
+  // padded
+  const int32_t* qlen;
+  const int32_t* dlen;
+  int64_t ncand;
+  int lq_max;
+  int ld_max;
+  // packed
+  const int32_t* qoff;
+  int64_t nq;
+  int64_t nd;
+  const int32_t* qids;
+  const int32_t* dids;
+  int64_t total_q;
+  // outputs
+  float* scores;
+  int32_t* argmax;
+};
+
+struct Pair {
+  int64_t q_row0;
+  int64_t d_row0;
+  int lq;
+  int ld;
+  bool ok;
+};
+
+// Resolve pair p to row ranges.  Every index read from device memory is
+// range-checked so invalid metadata never causes an out-of-bounds access.
+__device__ __forceinline__ Pair resolve_pair(const FwdArgs& a, int64_t p) {
+  Pair r{0, 0, 0, 0, false};
+  if (a.mode == kContrastive) {
+    const int64_t q = p / a.nb;
+    const int64_t b = p - q * a.nb;
+    const int64_t s = a.doff[b], e = a.doff[b + 1];
+    r.q_row0 = q * a.lq;
+    r.lq = a.lq;
+    r.d_row0 = s;
+    r.ld = (int)(e - s);
+    r.ok = (s >= 0) && (e > s) && (e <= a.total_d);
+  } else if (a.mode == kPadded) {
+    const int64_t b = p / a.ncand;
+    const int lq = a.qlen[b];
+    const int ld = a.dlen[p];
+    r.q_row0 = b * a.lq_max;
+    r.lq = lq;
+    r.d_row0 = p * a.ld_max;
+    r.ld = ld;
+    r.ok = (lq >= 1) && (lq <= a.lq_max) && (ld >= 1) && (ld <= a.ld_max);
+  } else {
+    const int64_t qi = a.qids[p], di = a.dids[p];
+    if (qi < 0 || qi >= a.nq || di < 0 || di >= a.nd) return r;
+    const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
+    const int64_t ds = a.doff[di], de = a.doff[di + 1];
+    r.q_row0 = qs;
+    r.lq = (int)(qe - qs);
+    r.d_row0 = ds;
+    r.ld = (int)(de - ds);
+    r.ok = (qs >= 0) && (qe > qs) && (qe <= a.total_q) && (qe - qs <= a.slots) &&
+           (ds >= 0) && (de > ds) && (de <= a.total_d);
+  }
+  return r;
+}
+
+__device__ __forceinline__ void write_invalid_pair(const FwdArgs& a, int64_t p,
+                                                   int lane) {
+  if (lane == 0) a.scores[p] = __builtin_nanf("");
+  if (a.argmax)
+    for (int t = lane; t < a.slots; t += 64) a.argmax[p * a.slots + t] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// pair_kernel: each wave scores a run of `ppw` consecutive pairs.
+// QB query blocks (32 tokens each) are held in registers; queries longer than
+// 32*QB tokens are processed QB blocks at a time, re-streaming the document.
+// ---------------------------------------------------------------------------
+template <typename T, int KS, int QB, bool ARGMAX>
+__global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
+                                                   bool vec) {
+  using S = typename T::storage;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t p_begin = wave * ppw;
+  if (p_begin >= a.npairs) return;
+  const int64_t p_end = min(p_begin + (int64_t)ppw, a.npairs);
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+
+  Frag<T> qf[QB][KS];
+  int64_t loaded_q = -1;
+  int loaded_lq = -1, loaded_g = -1;
+
+  for (int64_t p = p_begin; p < p_end; ++p) {
+    const Pair pr = resolve_pair(a, p);
+    if (!pr.ok) {
+      write_invalid_pair(a, p, lane);
+      continue;
+    }
+    const int nblk = (pr.lq + kTileCols - 1) / kTileCols;
+    const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
+    float score = 0.0f;
+    for (int g0 = 0; g0 < nblk; g0 += QB) {
+      if (pr.q_row0 != loaded_q || pr.lq != loaded_lq || g0 != loaded_g) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const int tok = min((g0 + qb) * kTileCols + c, pr.lq - 1);
+          const S* row = Q + (pr.q_row0 + tok) * (int64_t)dim;
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            qf[qb][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+        }
+        loaded_q = pr.q_row0;
+        loaded_lq = pr.lq;
+        loaded_g = g0;
+      }
+      float m[QB];
+      int am[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        m[qb] = -__builtin_inff();
+        am[qb] = 0;
+      }
+      Frag<T> df[KS];
+      {
+        const int r = min(c, pr.ld - 1);
+        const S* row = D + (pr.d_row0 + r) * (int64_t)dim;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          df[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+      }
+      for (int t = 0; t < ntiles; ++t) {
+        Frag<T> nf[KS];
+        if (t + 1 < ntiles) {
+          const int r = min((t + 1) * kTileRows + c, pr.ld - 1);
+          const S* row = D + (pr.d_row0 + r) * (int64_t)dim;
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            nf[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+        }
+        const int valid = pr.ld - t * kTileRows;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          f32x16 acc = {};
+#pragma unroll
+          for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc);
+          if (valid < kTileRows) mask_rows(acc, h, valid);
+          tile_update<ARGMAX>(acc, m[qb], am[qb], t * kTileRows + 4 * h);
+        }
+        if (t + 1 < ntiles) {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) df[s] = nf[s];
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int blk = g0 + qb;
+        if (blk < nblk) {
+          merge_halves(m[qb], am[qb]);
+          const int tok = blk * kTileCols + c;
+          const bool valid = tok < pr.lq;
+          score += half_sum(valid ? m[qb] : 0.0f);
+          if (ARGMAX && h == 0 && tok < a.slots)
+            a.argmax[p * a.slots + tok] = valid ? am[qb] : 0;
+        }
+      }
+    }
+    if (ARGMAX) {
+      for (int t = nblk * kTileCols + lane; t < a.slots; t += 64)
+        a.argmax[p * a.slots + t] = 0;
+    }
+    if (lane == 0) a.scores[p] = score;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// contrastive_tiled_kernel
+// ---------------------------------------------------------------------------
+// Workgroup = 8 waves.  Wave w holds NBW query blocks: queries
+// [q0 + w*qpw, q0 + (w+1)*qpw), each of nblk = ceil(Lq/32) blocks, with
+// qpw * nblk <= NBW.  Document tiles (32 rows x dim) are staged in LDS as
+// 16-byte pieces; piece index is XOR-swizzled with the row so the MFMA
+// operand reads (one row per lane) are bank-conflict free.
+constexpr int kTiledWaves = 8;
+constexpr int kTiledThreads = kTiledWaves * 64;
+
+struct TiledArgs {
+  const void* q;
+  const void* d;
+  const int32_t* doff;
+  int64_t nq;
+  int64_t nb;
+  int64_t total_d;
+  int lq;
+  int dim;
+  int nblk;   // blocks per query
+  int qpw;    // queries per wave
+  int n_qg;   // query groups
+  int dpw;    // documents per workgroup
+  int n_dc;   // document chunks
+  float* scores;
+  int32_t* argmax;
+};
+
+template <typename T, int KS>
+struct TileGeom {
+  static constexpr int kPieceElems = 16 / T::bytes;         // elements / 16 B
+  static constexpr int P = KS * kChunk / kPieceElems;       // pieces per row
+  static constexpr int SWZ = (P < 16 ? P : 16) - 1;
+  static constexpr int kPieces = kTileRows * P;             // per tile
+  static constexpr int NP = (kPieces + kTiledThreads - 1) / kTiledThreads;
+  static constexpr int kBufPieces = kPieces;                // uint4 per buffer
+};
+
+template <typename T, int KS, int NBW, bool ARGMAX>
+__global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(
+    TiledArgs a, bool vec) {
+  using S = typename T::storage;
+  using G = TileGeom<T, KS>;
+  extern __shared__ uint4 lds[];  // [2][32][P]
+
+  // XCD-aware mapping: consecutive hardware workgroup ids go round-robin over
+  // the 8 XCDs; give each XCD a contiguous range of logical ids, ordered
+  // query-group fastest, so the workgroups sharing a doc chunk share an L2.
+  const int64_t total = (int64_t)a.n_qg * a.n_dc;
+  const int64_t per_xcd = gridDim.x / 8;
+  const int64_t L = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (L >= total) return;
+  const int qg = (int)(L % a.n_qg);
+  const int dc = (int)(L / a.n_qg);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+
+  // ---- query blocks of this wave -> registers
+  const int64_t q_first = ((int64_t)qg * kTiledWaves + wave) * a.qpw;
+  Frag<T> qf[NBW][KS];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    int64_t q = q_first + j / a.nblk;
+    q = min(q, a.nq - 1);
+    const int part = j % a.nblk;
+    const int tok = min(part * kTileCols + c, a.lq - 1);
+    const S* row = Q + (q * a.lq + tok) * (int64_t)dim;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qf[j][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+  }
+
+  const int64_t b_begin = (int64_t)dc * a.dpw;
+  const int64_t b_end = min(b_begin + (int64_t)a.dpw, a.nb);
+
+  // Flattened walk over (doc, tile).  `cur_*` is the tile being computed,
+  // `nxt_*` the tile being fetched.
+  auto doc_len = [&](int64_t b, int64_t& s0) -> int {
+    const int64_t s = a.doff[b], e = a.doff[b + 1];
+    s0 = s;
+    const bool ok = (s >= 0) && (e > s) && (e <= a.total_d);
+    return ok ? (int)(e - s) : 0;
+  };
+
+  uint4 stage[G::NP];
+  auto fetch = [&](int64_t row0, int ld, int t) {
+#pragma unroll
+    for (int i = 0; i < G::NP; ++i) {
+      const int piece = tid + i * kTiledThreads;
+      stage[i] = make_uint4(0, 0, 0, 0);
+      if (piece < G::kPieces) {
+        const int r = piece / G::P;
+        const int pc = piece - r * G::P;
+        const int row = min(t * kTileRows + r, ld - 1);
+        const S* src = D + (row0 + row) * (int64_t)dim;
+        const int k0 = pc * G::kPieceElems;
+        if (vec) {
+          stage[i] = *reinterpret_cast<const uint4*>(src + k0);
+        } else {
+          if constexpr (T::bytes == 2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = k0 + 2 * e;
+              const uint32_t lo = (k < dim) ? (uint32_t)src[k] : 0u;
+              const uint32_t hi = (k + 1 < dim) ? (uint32_t)src[k + 1] : 0u;
+              w[e] = lo | (hi << 16);
+            }
+            stage[i] = make_uint4(w[0], w[1], w[2], w[3]);
+          } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w[e] = (k0 + e < dim) ? __float_as_uint(src[k0 + e]) : 0u;
+            stage[i] = make_uint4(w[0], w[1], w[2], w[3]);
+          }
+        }
+      }
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < G::NP; ++i) {
+      const int piece = tid + i * kTiledThreads;
+      if (piece < G::kPieces) {
+        const int r = piece / G::P;
+        const int pc = piece - r * G::P;
+        lds[buf * G::kBufPieces + r * G::P + (pc ^ (r & G::SWZ))] = stage[i];
+      }
+    }
+  };
+
+  // Find the first valid document of the chunk.
+  int64_t cur_b = b_begin, cur_row0 = 0;
+  int cur_ld = 0;
+  while (cur_b < b_end) {
+    cur_ld = doc_len(cur_b, cur_row0);
+    if (cur_ld > 0) break;
+    ++cur_b;
+  }
+  // Documents with invalid offsets get NaN scores / zero argmax.
+  auto write_invalid_doc = [&](int64_t b) {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      const int64_t q = q_first + j / a.nblk;
+      if (j >= a.qpw * a.nblk || q >= a.nq) continue;
+      const int part = j % a.nblk;
+      const int tok = part * kTileCols + c;
+      if (ARGMAX && h == 0 && tok < a.lq)
+        a.argmax[(q * a.nb + b) * a.lq + tok] = 0;
+      if (part == 0 && lane == 0) a.scores[q * a.nb + b] = __builtin_nanf("");
+    }
+  };
+  for (int64_t b = b_begin; b < cur_b; ++b) write_invalid_doc(b);
+  if (cur_b >= b_end) return;
+
+  fetch(cur_row0, cur_ld, 0);
+  commit(0);
+  __syncthreads();
+
+  int cur_t = 0;
+  int buf = 0;
+  float m[NBW];
+  int am[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    m[j] = -__builtin_inff();
+    am[j] = 0;
+  }
+
+  while (true) {
+    // ---- decide and fetch the next tile (may belong to the next doc)
+    const int cur_ntiles = (cur_ld + kTileRows - 1) / kTileRows;
+    int64_t nxt_b = cur_b, nxt_row0 = cur_row0;
+    int nxt_ld = cur_ld, nxt_t = cur_t + 1;
+    int64_t skipped_from = -1, skipped_to = -1;
+    if (nxt_t >= cur_ntiles) {
+      nxt_t = 0;
+      nxt_b = cur_b + 1;
+      skipped_from = nxt_b;
+      nxt_ld = 0;
+      while (nxt_b < b_end) {
+        nxt_ld = doc_len(nxt_b, nxt_row0);
+        if (nxt_ld > 0) break;
+        ++nxt_b;
+      }
+      skipped_to = nxt_b;
+    }
+    const bool have_next = nxt_b < b_end;
+    if (have_next) fetch(nxt_row0, nxt_ld, nxt_t);
+
+    // ---- compute on the current tile
+    Frag<T> df[KS];
+    const uint4* tile = lds + buf * G::kBufPieces + c * G::P;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (T::bytes == 2) {
+        df[s].v = tile[(2 * s + h) ^ (c & G::SWZ)];
+      } else {
+        df[s].lo = tile[(4 * s + 2 * h) ^ (c & G::SWZ)];
+        df[s].hi = tile[(4 * s + 2 * h + 1) ^ (c & G::SWZ)];
+      }
+    }
+    const int valid = cur_ld - cur_t * kTileRows;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+      f32x16 acc = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[j][s], acc);
+      if (valid < kTileRows) mask_rows(acc, h, valid);
+      tile_update<ARGMAX>(acc, m[j], am[j], cur_t * kTileRows + 4 * h);
+    }
+
+    // ---- end of document: finalize (query, doc) results
+    if (cur_t + 1 >= cur_ntiles) {
+      float part_sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int part = j % a.nblk;
+        const int64_t q = q_first + j / a.nblk;
+        merge_halves(m[j], am[j]);
+        const int tok = part * kTileCols + c;
+        const bool vtok = tok < a.lq;
+        const float s = half_sum(vtok ? m[j] : 0.0f);
+        part_sum = (part == 0) ? s : part_sum + s;
+        const bool q_ok = (j < a.qpw * a.nblk) && (q < a.nq);
+        if (q_ok) {
+          if (ARGMAX && h == 0 && vtok)
+            a.argmax[(q * a.nb + cur_b) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == 0)
+            a.scores[q * a.nb + cur_b] = part_sum;
+        }
+        m[j] = -__builtin_inff();
+        am[j] = 0;
+      }
+      for (int64_t b = skipped_from; b >= 0 && b < skipped_to; ++b)
+        write_invalid_doc(b);
+    }
+
+    if (!have_next) break;
+    commit(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    cur_b = nxt_b;
+    cur_row0 = nxt_row0;
+    cur_ld = nxt_ld;
+    cur_t = nxt_t;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side dispatch
+// ---------------------------------------------------------------------------
+static int ks_for_dim(int dim) {
+  if (dim <= 32) return 2;
+  if (dim <= 64) return 4;
+  if (dim <= 128) return 8;
+  return 16;
+}
+
+static bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+template <typename T, int KS, int QB>
+static void launch_pair_qb(const FwdArgs& a, int ppw, bool vec, dim3 grid,
+                           hipStream_t st) {
+  if (a.argmax)
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, true>), grid, dim3(256), 0, st,
+                       a, ppw, vec);
+  else
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, false>), grid, dim3(256), 0,
+                       st, a, ppw, vec);
+}
+
+template <typename T, int KS>
+static void launch_pair_ks(const FwdArgs& a, int max_lq, int ppw, bool vec,
+                           dim3 grid, hipStream_t st) {
+  // Two query blocks in registers unless that would not fit (fp32, dim 256).
+  constexpr bool kTwoFit = (KS * (T::bytes == 2 ? 4 : 8)) <= 64;
+  if (max_lq > kTileCols && kTwoFit)
+    launch_pair_qb<T, KS, (kTwoFit ? 2 : 1)>(a, ppw, vec, grid, st);
+  else
+    launch_pair_qb<T, KS, 1>(a, ppw, vec, grid, st);
+}
+
+template <typename T>
+static void launch_pair(const FwdArgs& a, int max_lq, int ppw, bool vec,
+                        hipStream_t st) {
+  const int64_t waves = (a.npairs + ppw - 1) / ppw;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  switch (ks_for_dim(a.dim)) {
+    case 2: launch_pair_ks<T, 2>(a, max_lq, ppw, vec, grid, st); break;
+    case 4: launch_pair_ks<T, 4>(a, max_lq, ppw, vec, grid, st); break;
+    case 8: launch_pair_ks<T, 8>(a, max_lq, ppw, vec, grid, st); break;
+    default: launch_pair_ks<T, 16>(a, max_lq, ppw, vec, grid, st); break;
+  }
+}
+
+static int pairs_per_wave(int64_t npairs) {
+  // Aim for ~8k waves (32 per CU) so the chip stays full; never below 1.
+  int64_t ppw = (npairs + 8191) / 8192;
+  if (ppw < 1) ppw = 1;
+  if (ppw > 64) ppw = 64;
+  return (int)ppw;
+}
+
+static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
+                    hipStream_t st) {
+  const int ppw = pairs_per_wave(a.npairs);
+  const bool vec = (a.dim == ks_for_dim(a.dim) * kChunk) && aligned16(a.q) &&
+                   aligned16(a.d);
+  switch (dtype) {
+    case MAXSIM_BFLOAT16: launch_pair<BF16>(a, max_lq, ppw, vec, st); break;
+    case MAXSIM_FLOAT16: launch_pair<F16>(a, max_lq, ppw, vec, st); break;
+    default: launch_pair<F32>(a, max_lq, ppw, vec, st); break;
+  }
+  return check_launch("pair_kernel");
+}
+
+// Blocks per wave for the tiled kernel, per (dtype width, KS): the query
+// fragments (NBW * KS * {4,8} VGPRs) must leave room for the document
+// fragments and accumulators at two waves per SIMD.
+template <typename T, int KS>
+constexpr int tiled_nbw() {
+  return (KS * (T::bytes == 2 ? 4 : 8) * 2 <= 64) ? 2 : 1;
+}
+
+template <typename T, int KS>
+static void launch_tiled_ks(TiledArgs a, bool vec, hipStream_t st) {
+  constexpr int NBW = tiled_nbw<T, KS>();
+  using G = TileGeom<T, KS>;
+  a.qpw = NBW / a.nblk;
+  const int64_t q_per_wg = (int64_t)a.qpw * kTiledWaves;
+  a.n_qg = (int)((a.nq + q_per_wg - 1) / q_per_wg);
+  // Enough workgroups to fill 256 CUs several times over, but keep chunks of
+  // documents together so every workgroup streams a long tile sequence.
+  int64_t n_dc = (2048 + a.n_qg - 1) / a.n_qg;
+  if (n_dc > a.nb) n_dc = a.nb;
+  if (n_dc < 1) n_dc = 1;
+  a.dpw = (int)((a.nb + n_dc - 1) / n_dc);
+  a.n_dc = (int)((a.nb + a.dpw - 1) / a.dpw);
+  const int64_t total = (int64_t)a.n_qg * a.n_dc;
+  const int64_t per_xcd = (total + 7) / 8;
+  const dim3 grid((unsigned)(per_xcd * 8));
+  const size_t lds = 2 * G::kBufPieces * sizeof(uint4);
+  if (a.argmax)
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
+                       dim3(kTiledThreads), lds, st, a, vec);
+  else
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false>), grid,
+                       dim3(kTiledThreads), lds, st, a, vec);
+}
+
+template <typename T>
+static bool tiled_supported(int dim, int lq) {
+  const int ks = ks_for_dim(dim);
+  int nbw = 1;
+  switch (ks) {
+    case 2: nbw = tiled_nbw<T, 2>(); break;
+    case 4: nbw = tiled_nbw<T, 4>(); break;
+    case 8: nbw = tiled_nbw<T, 8>(); break;
+    default: nbw = tiled_nbw<T, 16>(); break;
+  }
+  const int nblk = (lq + kTileCols - 1) / kTileCols;
+  return nblk <= nbw;
+}
+
+template <typename T>
+static void launch_tiled(const TiledArgs& a, bool vec, hipStream_t st) {
+  switch (ks_for_dim(a.dim)) {
+    case 2: launch_tiled_ks<T, 2>(a, vec, st); break;
+    case 4: launch_tiled_ks<T, 4>(a, vec, st); break;
+    case 8: launch_tiled_ks<T, 8>(a, vec, st); break;
+    default: launch_tiled_ks<T, 16>(a, vec, st); break;
+  }
+}
+
+static int run_contrastive(maxsim_dtype dtype, const void* q, int64_t nq,
+                           int64_t lq, const void* d, int64_t total_d,
+                           const int32_t* doff, int64_t nb, int64_t dim,
+                           float* scores, int32_t* argmax, hipStream_t st) {
+  const bool vec = (dim == ks_for_dim((int)dim) * kChunk) && aligned16(q) &&
+                   aligned16(d);
+  bool tiled = false;
+  switch (dtype) {
+    case MAXSIM_BFLOAT16: tiled = tiled_supported<BF16>((int)dim, (int)lq); break;
+    case MAXSIM_FLOAT16: tiled = tiled_supported<F16>((int)dim, (int)lq); break;
+    default: tiled = tiled_supported<F32>((int)dim, (int)lq); break;
+  }
+  if (tiled) {
+    TiledArgs a{};
+    a.q = q;
+    a.d = d;
+    a.doff = doff;
+    a.nq = nq;
+    a.nb = nb;
+    a.total_d = total_d;
+    a.lq = (int)lq;
+    a.dim = (int)dim;
+    a.nblk = (int)((lq + kTileCols - 1) / kTileCols);
+    a.scores = scores;
+    a.argmax = argmax;
+    switch (dtype) {
+      case MAXSIM_BFLOAT16: launch_tiled<BF16>(a, vec, st); break;
+      case MAXSIM_FLOAT16: launch_tiled<F16>(a, vec, st); break;
+      default: launch_tiled<F32>(a, vec, st); break;
+    }
+    return check_launch("contrastive_tiled_kernel");
+  }
+  FwdArgs a{};
+  a.q = q;
+  a.d = d;
+  a.dim = (int)dim;
+  a.mode = kContrastive;
+  a.npairs = nq * nb;
+  a.slots = (int)lq;
+  a.nb = nb;
+  a.lq = (int)lq;
+  a.doff = doff;
+  a.total_d = total_d;
+  a.scores = scores;
+  a.argmax = argmax;
+  return run_pair(a, dtype, (int)lq, st);
+}
+
+}  // namespace maxsim
+
+using namespace maxsim;
+
+// ---------------------------------------------------------------------------
+// C ABI -- forward entry points
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int maxsim_amd_contrastive_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, int64_t num_queries, int64_t Lq,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents, int64_t dim,
+    float* scores, int32_t* argmax, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  if (num_queries < 0 || num_documents < 0 || total_d_tokens < 0)
+    return fail(MAXSIM_ERR_INVALID, "negative size");
+  if (Lq <= 0) return fail(MAXSIM_ERR_INVALID, "Lq must be > 0; got %lld", (long long)Lq);
+  if (int e = check_dim(dim)) return e;
+  if (num_queries == 0 || num_documents == 0) return MAXSIM_OK;
+  if (!queries || !documents || !document_offsets || !scores)
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  if (num_queries * num_documents > (int64_t)1 << 40 || Lq > (1 << 20))
+    return fail(MAXSIM_ERR_UNSUPPORTED, "problem too large");
+  return run_contrastive(dtype, queries, num_queries, Lq, documents,
+                         total_d_tokens, document_offsets, num_documents, dim,
+                         scores, argmax, static_cast<hipStream_t>(stream));
+}
+
+int maxsim_amd_contrastive_forward(maxsim_dtype dtype, const void* queries,
+                                   int64_t num_queries, int64_t Lq,
+                                   const void* documents,
+                                   int64_t total_d_tokens,
+                                   const int32_t* document_offsets,
+                                   int64_t num_documents, int64_t dim,
+                                   float* scores, void* stream) {
+  return maxsim_amd_contrastive_forward_with_argmax(
+      dtype, queries, num_queries, Lq, documents, total_d_tokens,
+      document_offsets, num_documents, dim, scores, nullptr, stream);
+}
+
+int maxsim_amd_padded_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, const int32_t* query_lengths,
+    const void* documents, const int32_t* doc_lengths, int64_t batch,
+    int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
+    float* scores, int32_t* argmax, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  if (batch < 0 || num_candidates < 0)
+    return fail(MAXSIM_ERR_INVALID, "negative size");
+  if (Lq_max <= 0 || Ld_max <= 0)
+    return fail(MAXSIM_ERR_INVALID, "Lq_max and Ld_max must be > 0");
+  if (int e = check_dim(dim)) return e;
+  if (batch == 0 || num_candidates == 0) return MAXSIM_OK;
+  if (!queries || !documents || !query_lengths || !doc_lengths || !scores)
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  if (Lq_max > (1 << 20) || Ld_max > ((int64_t)1 << 30))
+    return fail(MAXSIM_ERR_UNSUPPORTED, "padded extent too large");
+  FwdArgs a{};
+  a.q = queries;
+  a.d = documents;
+  a.dim = (int)dim;
+  a.mode = kPadded;
+  a.npairs = batch * num_candidates;
+  a.slots = (int)Lq_max;
+  a.qlen = query_lengths;
+  a.dlen = doc_lengths;
+  a.ncand = num_candidates;
+  a.lq_max = (int)Lq_max;
+  a.ld_max = (int)Ld_max;
+  a.scores = scores;
+  a.argmax = argmax;
+  return run_pair(a, dtype, (int)Lq_max, static_cast<hipStream_t>(stream));
+}
+
+int maxsim_amd_padded_forward(maxsim_dtype dtype, const void* queries,
+                              const int32_t* query_lengths,
+                              const void* documents,
+                              const int32_t* doc_lengths, int64_t batch,
+                              int64_t num_candidates, int64_t Lq_max,
+                              int64_t Ld_max, int64_t dim, float* scores,
+                              void* stream) {
+  return maxsim_amd_padded_forward_with_argmax(
+      dtype, queries, query_lengths, documents, doc_lengths, batch,
+      num_candidates, Lq_max, Ld_max, dim, scores, nullptr, stream);
+}
+
+int maxsim_amd_packed_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
+    const int32_t* query_offsets, int64_t num_queries, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* pair_query_ids,
+    const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
+    int64_t max_q_len, float* scores, int32_t* argmax, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
+      num_documents < 0 || num_pairs < 0)
+    return fail(MAXSIM_ERR_INVALID, "negative size");
+  if (max_q_len <= 0)
+    return fail(MAXSIM_ERR_INVALID, "max_q_len must be > 0; got %lld",
+                (long long)max_q_len);
+  if (int e = check_dim(dim)) return e;
+  if (num_pairs == 0) return MAXSIM_OK;
+  if (!queries || !documents || !query_offsets || !document_offsets ||
+      !pair_query_ids || !pair_document_ids || !scores)
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  if (max_q_len > (1 << 20))
+    return fail(MAXSIM_ERR_UNSUPPORTED, "max_q_len too large");
+  FwdArgs a{};
+  a.q = queries;
+  a.d = documents;
+  a.dim = (int)dim;
+  a.mode = kPacked;
+  a.npairs = num_pairs;
+  a.slots = (int)max_q_len;
+  a.qoff = query_offsets;
+  a.nq = num_queries;
+  a.doff = document_offsets;
+  a.nd = num_documents;
+  a.qids = pair_query_ids;
+  a.dids = pair_document_ids;
+  a.total_q = total_q_tokens;
+  a.total_d = total_d_tokens;
+  a.scores = scores;
+  a.argmax = argmax;
+  return run_pair(a, dtype, (int)max_q_len, static_cast<hipStream_t>(stream));
+}
+
+int maxsim_amd_forward(maxsim_dtype dtype, const void* queries,
+                       int64_t total_q_tokens, const int32_t* query_offsets,
+                       int64_t num_queries, const void* documents,
+                       int64_t total_d_tokens, const int32_t* document_offsets,
+                       int64_t num_documents, const int32_t* pair_query_ids,
+                       const int32_t* pair_document_ids, int64_t num_pairs,
+                       int64_t dim, int64_t max_q_len, float* scores,
+                       void* stream) {
+  return maxsim_amd_packed_forward_with_argmax(
+      dtype, queries, total_q_tokens, query_offsets, num_queries, documents,
+      total_d_tokens, document_offsets, num_documents, pair_query_ids,
+      pair_document_ids, num_pairs, dim, max_q_len, scores, nullptr, stream);
+}
+
+}  // extern "C"

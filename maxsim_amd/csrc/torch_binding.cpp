@@ -1,0 +1,415 @@
+// Thin torch binding over the C ABI (include/maxsim_amd.h).
+//
+// Registers the reference's nine operator schemas (torch-ext/torch_binding.cpp
+// :7-90) under the `maxsim_amd` namespace for the CUDA dispatch key, which is
+// the key PyTorch-ROCm uses for HIP devices.  Each op checks its tensors the
+// way the reference host functions do (maxsim.cu:819-2286; TORCH_CHECK ->
+// RuntimeError), makes inputs contiguous and int32, allocates the outputs
+// with the caching allocator and calls the C ABI on the current HIP stream.
+// The C ABI itself never allocates.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <tuple>
+#include <vector>
+
+#include "../../include/maxsim_amd.h"
+
+namespace {
+
+using at::Tensor;
+
+maxsim_dtype to_dtype(const Tensor& t) {
+  switch (t.scalar_type()) {
+    case at::kFloat: return MAXSIM_FLOAT32;
+    case at::kHalf: return MAXSIM_FLOAT16;
+    case at::kBFloat16: return MAXSIM_BFLOAT16;
+    default:
+      TORCH_CHECK(false,
+                  "queries/documents dtype must be float32, float16, or bfloat16; got ",
+                  t.scalar_type());
+  }
+  return MAXSIM_FLOAT32;
+}
+
+void check_status(int rc) {
+  TORCH_CHECK(rc == MAXSIM_OK, "maxsim_amd: ", maxsim_amd_last_error());
+}
+
+void* current_stream(const Tensor& t) {
+  return reinterpret_cast<void*>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
+}
+
+Tensor as_i32(const Tensor& t) {
+  TORCH_CHECK(t.scalar_type() == at::kInt || t.scalar_type() == at::kLong,
+              "index tensors must be int32 or int64; got ", t.scalar_type());
+  return t.contiguous().to(at::kInt);
+}
+
+void check_embeddings(const Tensor& q, const Tensor& d) {
+  TORCH_CHECK(q.device().is_cuda(), "queries must be a HIP (torch 'cuda') tensor");
+  TORCH_CHECK(d.device() == q.device(),
+              "documents must be on the same device as queries");
+  TORCH_CHECK(q.scalar_type() == d.scalar_type(),
+              "queries and documents must have the same dtype");
+}
+
+void check_on(const Tensor& t, const Tensor& q, const char* name) {
+  TORCH_CHECK(t.device() == q.device(), name,
+              " must be on the same device as queries");
+}
+
+at::TensorOptions f32_opts(const Tensor& q) {
+  return at::TensorOptions().dtype(at::kFloat).device(q.device());
+}
+at::TensorOptions i32_opts(const Tensor& q) {
+  return at::TensorOptions().dtype(at::kInt).device(q.device());
+}
+
+// ---- packed ---------------------------------------------------------------
+
+// max_q_len < 0: validate offsets and ids on the host and infer the maximum
+// query segment length (reference maxsim.cu:851-890, same messages).
+int64_t host_validate_packed(const Tensor& qoff, int64_t total_q, const Tensor& doff,
+                             int64_t total_d, const Tensor& qids, const Tensor& dids) {
+  auto check_offsets = [](const Tensor& off, int64_t total, const char* name) {
+    auto c = off.to(at::kCPU).to(at::kLong).contiguous();
+    const int64_t* p = c.data_ptr<int64_t>();
+    const int64_t n = c.numel();
+    TORCH_CHECK(n >= 2, name, " must have length >= 2");
+    TORCH_CHECK(p[0] == 0, name, "[0] must equal 0, got ", p[0]);
+    TORCH_CHECK(p[n - 1] == total, name, "[-1] (", p[n - 1],
+                ") must equal total token count (", total, ")");
+    int64_t m = 0;
+    for (int64_t i = 0; i + 1 < n; ++i) {
+      const int64_t diff = p[i + 1] - p[i];
+      TORCH_CHECK(diff > 0, "empty segment in ", name, " at index ", i);
+      m = std::max(m, diff);
+    }
+    return std::make_pair(m, n - 1);
+  };
+  auto check_ids = [](const Tensor& ids, int64_t upper, const char* name) {
+    auto c = ids.to(at::kCPU).to(at::kLong).contiguous();
+    const int64_t* p = c.data_ptr<int64_t>();
+    for (int64_t i = 0; i < c.numel(); ++i)
+      TORCH_CHECK(p[i] >= 0 && p[i] < upper, name, "[", i, "] = ", p[i],
+                  " out of range [0, ", upper, ")");
+  };
+  auto [mql, nq] = check_offsets(qoff, total_q, "query_offsets");
+  auto [unused, nd] = check_offsets(doff, total_d, "document_offsets");
+  (void)unused;
+  check_ids(qids, nq, "pair_query_ids");
+  check_ids(dids, nd, "pair_document_ids");
+  return mql;
+}
+
+struct Packed {
+  Tensor q, qoff, d, doff, qids, dids;
+  int64_t mql;
+};
+
+Packed prep_packed(Tensor queries, Tensor query_offsets, Tensor documents,
+                   Tensor document_offsets, Tensor pair_query_ids,
+                   Tensor pair_document_ids, int64_t max_q_len) {
+  check_embeddings(queries, documents);
+  TORCH_CHECK(queries.dim() == 2 && documents.dim() == 2,
+              "queries/documents must be 2-D [tokens, dim]");
+  TORCH_CHECK(queries.size(1) == documents.size(1),
+              "queries.dim must match documents.dim");
+  check_on(query_offsets, queries, "query_offsets");
+  check_on(document_offsets, queries, "document_offsets");
+  check_on(pair_query_ids, queries, "pair_query_ids");
+  check_on(pair_document_ids, queries, "pair_document_ids");
+  TORCH_CHECK(pair_query_ids.dim() == 1 && pair_query_ids.sizes() == pair_document_ids.sizes(),
+              "pair_query_ids and pair_document_ids must be 1-D with the same shape");
+  Packed p;
+  p.q = queries.contiguous();
+  p.d = documents.contiguous();
+  p.qoff = as_i32(query_offsets);
+  p.doff = as_i32(document_offsets);
+  p.qids = as_i32(pair_query_ids);
+  p.dids = as_i32(pair_document_ids);
+  if (max_q_len < 0) {
+    p.mql = host_validate_packed(p.qoff, p.q.size(0), p.doff, p.d.size(0), p.qids, p.dids);
+  } else {
+    TORCH_CHECK(max_q_len > 0, "max_q_len must be > 0; got ", max_q_len);
+    p.mql = max_q_len;
+  }
+  return p;
+}
+
+Tensor maxsim_forward(Tensor queries, Tensor query_offsets, Tensor documents,
+                      Tensor document_offsets, Tensor pair_query_ids,
+                      Tensor pair_document_ids, int64_t max_q_len) {
+  Packed p = prep_packed(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, max_q_len);
+  const int64_t np = p.qids.numel();
+  Tensor scores = at::empty({np}, f32_opts(p.q));
+  if (np == 0) return scores;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_forward(
+      to_dtype(p.q), p.q.data_ptr(), p.q.size(0), p.qoff.data_ptr<int32_t>(),
+      p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0), p.doff.data_ptr<int32_t>(),
+      p.doff.numel() - 1, p.qids.data_ptr<int32_t>(), p.dids.data_ptr<int32_t>(), np,
+      p.q.size(1), p.mql, scores.data_ptr<float>(), current_stream(p.q)));
+  return scores;
+}
+
+std::tuple<Tensor, Tensor> maxsim_packed_forward_with_argmax(
+    Tensor queries, Tensor query_offsets, Tensor documents, Tensor document_offsets,
+    Tensor pair_query_ids, Tensor pair_document_ids, int64_t max_q_len) {
+  TORCH_CHECK(max_q_len > 0, "max_q_len must be > 0");
+  Packed p = prep_packed(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, max_q_len);
+  const int64_t np = p.qids.numel();
+  Tensor scores = at::empty({np}, f32_opts(p.q));
+  Tensor argmax = at::empty({np, p.mql}, i32_opts(p.q));
+  if (np == 0) return {scores, argmax};
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_packed_forward_with_argmax(
+      to_dtype(p.q), p.q.data_ptr(), p.q.size(0), p.qoff.data_ptr<int32_t>(),
+      p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0), p.doff.data_ptr<int32_t>(),
+      p.doff.numel() - 1, p.qids.data_ptr<int32_t>(), p.dids.data_ptr<int32_t>(), np,
+      p.q.size(1), p.mql, scores.data_ptr<float>(), argmax.data_ptr<int32_t>(),
+      current_stream(p.q)));
+  return {scores, argmax};
+}
+
+std::tuple<Tensor, Tensor> maxsim_packed_backward(
+    Tensor dscore, Tensor queries, Tensor query_offsets, Tensor documents,
+    Tensor document_offsets, Tensor pair_query_ids, Tensor pair_document_ids,
+    Tensor argmax, int64_t max_q_len) {
+  TORCH_CHECK(max_q_len > 0, "max_q_len must be > 0");
+  Packed p = prep_packed(queries, query_offsets, documents, document_offsets,
+                         pair_query_ids, pair_document_ids, max_q_len);
+  TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
+  TORCH_CHECK(argmax.scalar_type() == at::kInt, "argmax must be int32");
+  check_on(dscore, p.q, "dscore");
+  check_on(argmax, p.q, "argmax");
+  const int64_t np = p.qids.numel();
+  TORCH_CHECK(dscore.numel() == np, "dscore must have num_pairs elements");
+  TORCH_CHECK(argmax.numel() == np * p.mql, "argmax must be [num_pairs, max_q_len]");
+  Tensor g = dscore.contiguous();
+  Tensor am = argmax.contiguous();
+  Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, f32_opts(p.q));
+  Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, f32_opts(p.q));
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_packed_backward(
+      to_dtype(p.q), g.data_ptr<float>(), p.q.data_ptr(), p.q.size(0),
+      p.qoff.data_ptr<int32_t>(), p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0),
+      p.doff.data_ptr<int32_t>(), p.doff.numel() - 1, p.qids.data_ptr<int32_t>(),
+      p.dids.data_ptr<int32_t>(), np, am.data_ptr<int32_t>(), p.mql, p.q.size(1),
+      dq.data_ptr<float>(), dd.data_ptr<float>(), current_stream(p.q)));
+  return {dq, dd};
+}
+
+// ---- padded ---------------------------------------------------------------
+
+struct Padded {
+  Tensor q, d, qlen, dlen;
+  int64_t B, C;
+};
+
+Padded prep_padded(Tensor queries, Tensor query_lengths, Tensor documents,
+                   Tensor doc_lengths, int64_t Lq_max, int64_t Ld_max,
+                   int64_t num_candidates) {
+  check_embeddings(queries, documents);
+  TORCH_CHECK(queries.dim() == 2 && documents.dim() == 2,
+              "queries/documents must be 2-D [rows, dim]");
+  TORCH_CHECK(queries.size(1) == documents.size(1),
+              "queries.dim must match documents.dim");
+  TORCH_CHECK(Lq_max > 0 && Ld_max > 0 && num_candidates > 0,
+              "Lq_max, Ld_max and num_candidates must be > 0");
+  check_on(query_lengths, queries, "query_lengths");
+  check_on(doc_lengths, queries, "doc_lengths");
+  Padded p;
+  p.q = queries.contiguous();
+  p.d = documents.contiguous();
+  TORCH_CHECK(p.q.size(0) % Lq_max == 0, "queries rows must be a multiple of Lq_max");
+  TORCH_CHECK(p.d.size(0) % Ld_max == 0, "documents rows must be a multiple of Ld_max");
+  p.B = p.q.size(0) / Lq_max;
+  p.C = num_candidates;
+  TORCH_CHECK(p.d.size(0) / Ld_max == p.B * p.C,
+              "documents rows must equal B * num_candidates * Ld_max");
+  p.qlen = as_i32(query_lengths);
+  p.dlen = as_i32(doc_lengths);
+  TORCH_CHECK(p.qlen.numel() == p.B, "query_lengths must have B elements");
+  TORCH_CHECK(p.dlen.numel() == p.B * p.C, "doc_lengths must have B * C elements");
+  return p;
+}
+
+Tensor maxsim_padded_forward(Tensor queries, Tensor query_lengths, Tensor documents,
+                             Tensor doc_lengths, int64_t Lq_max, int64_t Ld_max,
+                             int64_t num_candidates) {
+  Padded p = prep_padded(queries, query_lengths, documents, doc_lengths, Lq_max,
+                         Ld_max, num_candidates);
+  Tensor scores = at::empty({p.B * p.C}, f32_opts(p.q));
+  if (p.B * p.C == 0) return scores;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_padded_forward(
+      to_dtype(p.q), p.q.data_ptr(), p.qlen.data_ptr<int32_t>(), p.d.data_ptr(),
+      p.dlen.data_ptr<int32_t>(), p.B, p.C, Lq_max, Ld_max, p.q.size(1),
+      scores.data_ptr<float>(), current_stream(p.q)));
+  return scores;
+}
+
+std::tuple<Tensor, Tensor> maxsim_padded_forward_with_argmax(
+    Tensor queries, Tensor query_lengths, Tensor documents, Tensor doc_lengths,
+    int64_t Lq_max, int64_t Ld_max, int64_t num_candidates) {
+  Padded p = prep_padded(queries, query_lengths, documents, doc_lengths, Lq_max,
+                         Ld_max, num_candidates);
+  Tensor scores = at::empty({p.B * p.C}, f32_opts(p.q));
+  Tensor argmax = at::empty({p.B * p.C, Lq_max}, i32_opts(p.q));
+  if (p.B * p.C == 0) return {scores, argmax};
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_padded_forward_with_argmax(
+      to_dtype(p.q), p.q.data_ptr(), p.qlen.data_ptr<int32_t>(), p.d.data_ptr(),
+      p.dlen.data_ptr<int32_t>(), p.B, p.C, Lq_max, Ld_max, p.q.size(1),
+      scores.data_ptr<float>(), argmax.data_ptr<int32_t>(), current_stream(p.q)));
+  return {scores, argmax};
+}
+
+std::tuple<Tensor, Tensor> maxsim_padded_backward(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor query_lengths,
+    Tensor doc_lengths, Tensor argmax, int64_t Lq_max, int64_t Ld_max,
+    int64_t num_candidates) {
+  Padded p = prep_padded(queries, query_lengths, documents, doc_lengths, Lq_max,
+                         Ld_max, num_candidates);
+  TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
+  TORCH_CHECK(argmax.scalar_type() == at::kInt, "argmax must be int32");
+  check_on(dscore, p.q, "dscore");
+  check_on(argmax, p.q, "argmax");
+  TORCH_CHECK(argmax.numel() == p.B * p.C * Lq_max, "argmax must be [B*C, Lq_max]");
+  TORCH_CHECK(dscore.numel() == p.B * p.C, "dscore must have B*C elements");
+  Tensor g = dscore.contiguous();
+  Tensor am = argmax.contiguous();
+  Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, f32_opts(p.q));
+  Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, f32_opts(p.q));
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  check_status(maxsim_amd_padded_backward(
+      to_dtype(p.q), g.data_ptr<float>(), p.q.data_ptr(), p.d.data_ptr(),
+      p.qlen.data_ptr<int32_t>(), p.dlen.data_ptr<int32_t>(), am.data_ptr<int32_t>(),
+      p.B, p.C, Lq_max, Ld_max, p.q.size(1), dq.data_ptr<float>(),
+      dd.data_ptr<float>(), current_stream(p.q)));
+  return {dq, dd};
+}
+
+// ---- contrastive ----------------------------------------------------------
+
+struct Contrastive {
+  Tensor q, d, off;
+};
+
+Contrastive prep_contrastive(Tensor queries, Tensor documents, Tensor document_offsets) {
+  check_embeddings(queries, documents);
+  TORCH_CHECK(queries.dim() == 3, "queries must be [Nq, Lq, D]");
+  TORCH_CHECK(documents.dim() == 2, "documents must be [total_d_tokens, D]");
+  TORCH_CHECK(document_offsets.dim() == 1, "document_offsets must be 1-D");
+  TORCH_CHECK(queries.size(2) == documents.size(1),
+              "queries.D must match documents.D");
+  check_on(document_offsets, queries, "document_offsets");
+  TORCH_CHECK(document_offsets.numel() >= 1, "document_offsets must have at least 1 element");
+  TORCH_CHECK(queries.size(1) > 0, "Lq must be > 0");
+  TORCH_CHECK(queries.size(2) > 0, "dim must be > 0");
+  Contrastive c;
+  c.q = queries.contiguous();
+  c.d = documents.contiguous();
+  c.off = as_i32(document_offsets);
+  return c;
+}
+
+Tensor maxsim_contrastive_forward(Tensor queries, Tensor documents,
+                                  Tensor document_offsets) {
+  Contrastive c = prep_contrastive(queries, documents, document_offsets);
+  const int64_t Nq = c.q.size(0), Lq = c.q.size(1), Nb = c.off.numel() - 1;
+  Tensor scores = at::empty({Nq, Nb}, f32_opts(c.q));
+  if (Nq * Nb == 0) return scores;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
+  check_status(maxsim_amd_contrastive_forward(
+      to_dtype(c.q), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(), c.d.size(0),
+      c.off.data_ptr<int32_t>(), Nb, c.q.size(2), scores.data_ptr<float>(),
+      current_stream(c.q)));
+  return scores;
+}
+
+std::tuple<Tensor, Tensor> maxsim_contrastive_forward_with_argmax(
+    Tensor queries, Tensor documents, Tensor document_offsets) {
+  Contrastive c = prep_contrastive(queries, documents, document_offsets);
+  const int64_t Nq = c.q.size(0), Lq = c.q.size(1), Nb = c.off.numel() - 1;
+  Tensor scores = at::empty({Nq, Nb}, f32_opts(c.q));
+  Tensor argmax = at::empty({Nq, Nb, Lq}, i32_opts(c.q));
+  if (Nq * Nb == 0) return {scores, argmax};
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
+  check_status(maxsim_amd_contrastive_forward_with_argmax(
+      to_dtype(c.q), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(), c.d.size(0),
+      c.off.data_ptr<int32_t>(), Nb, c.q.size(2), scores.data_ptr<float>(),
+      argmax.data_ptr<int32_t>(), current_stream(c.q)));
+  return {scores, argmax};
+}
+
+std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
+    Tensor argmax) {
+  Contrastive c = prep_contrastive(queries, documents, document_offsets);
+  const int64_t Nq = c.q.size(0), Lq = c.q.size(1), Nb = c.off.numel() - 1;
+  TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
+  TORCH_CHECK(argmax.scalar_type() == at::kInt, "argmax must be int32");
+  check_on(dscore, c.q, "dscore");
+  check_on(argmax, c.q, "argmax");
+  TORCH_CHECK(dscore.numel() == Nq * Nb, "dscore must be [Nq, Nb]");
+  TORCH_CHECK(argmax.numel() == Nq * Nb * Lq, "argmax must be [Nq, Nb, Lq]");
+  Tensor g = dscore.contiguous();
+  Tensor am = argmax.contiguous();
+  Tensor dq = at::empty({Nq, Lq, c.q.size(2)}, f32_opts(c.q));
+  Tensor dd = at::empty({c.d.size(0), c.d.size(1)}, f32_opts(c.q));
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
+  check_status(maxsim_amd_contrastive_backward(
+      to_dtype(c.q), g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(),
+      c.d.size(0), c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(), c.q.size(2),
+      dq.data_ptr<float>(), dd.data_ptr<float>(), current_stream(c.q)));
+  return {dq, dd};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(maxsim_amd, m) {
+  m.def("maxsim_forward(Tensor queries, Tensor query_offsets, Tensor documents, "
+        "Tensor document_offsets, Tensor pair_query_ids, Tensor pair_document_ids, "
+        "int max_q_len) -> Tensor");
+  m.def("maxsim_padded_forward(Tensor queries, Tensor query_lengths, Tensor documents, "
+        "Tensor doc_lengths, int Lq_max, int Ld_max, int num_candidates) -> Tensor");
+  m.def("maxsim_padded_forward_with_argmax(Tensor queries, Tensor query_lengths, "
+        "Tensor documents, Tensor doc_lengths, int Lq_max, int Ld_max, "
+        "int num_candidates) -> (Tensor, Tensor)");
+  m.def("maxsim_padded_backward(Tensor dscore, Tensor queries, Tensor documents, "
+        "Tensor query_lengths, Tensor doc_lengths, Tensor argmax, int Lq_max, "
+        "int Ld_max, int num_candidates) -> (Tensor, Tensor)");
+  m.def("maxsim_packed_forward_with_argmax(Tensor queries, Tensor query_offsets, "
+        "Tensor documents, Tensor document_offsets, Tensor pair_query_ids, "
+        "Tensor pair_document_ids, int max_q_len) -> (Tensor, Tensor)");
+  m.def("maxsim_packed_backward(Tensor dscore, Tensor queries, Tensor query_offsets, "
+        "Tensor documents, Tensor document_offsets, Tensor pair_query_ids, "
+        "Tensor pair_document_ids, Tensor argmax, int max_q_len) -> (Tensor, Tensor)");
+  m.def("maxsim_contrastive_forward(Tensor queries, Tensor documents, "
+        "Tensor document_offsets) -> Tensor");
+  m.def("maxsim_contrastive_forward_with_argmax(Tensor queries, Tensor documents, "
+        "Tensor document_offsets) -> (Tensor, Tensor)");
+  m.def("maxsim_contrastive_backward(Tensor dscore, Tensor queries, Tensor documents, "
+        "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
+  m.impl("maxsim_forward", &maxsim_forward);
+  m.impl("maxsim_padded_forward", &maxsim_padded_forward);
+  m.impl("maxsim_padded_forward_with_argmax", &maxsim_padded_forward_with_argmax);
+  m.impl("maxsim_padded_backward", &maxsim_padded_backward);
+  m.impl("maxsim_packed_forward_with_argmax", &maxsim_packed_forward_with_argmax);
+  m.impl("maxsim_packed_backward", &maxsim_packed_backward);
+  m.impl("maxsim_contrastive_forward", &maxsim_contrastive_forward);
+  m.impl("maxsim_contrastive_forward_with_argmax",
+         &maxsim_contrastive_forward_with_argmax);
+  m.impl("maxsim_contrastive_backward", &maxsim_contrastive_backward);
+}

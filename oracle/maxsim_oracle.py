@@ -1,0 +1,192 @@
+"""CPU oracle for MaxSim -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this module, and only as the checker; the product
+(``maxsim_amd``) never imports or calls it.
+
+It restates, in numpy float64, the semantics the reference's kernels and
+tests fix for the operator family:
+
+* score(q, d) = sum over valid query tokens i of max over valid document
+  tokens j of <q_i, d_j>                     (reference.py:20-32, README.md:26-36)
+* argmax: ascending j with a strict ``>`` -> the FIRST maximal index wins
+  ties                                        (reference.py:35-47, maxsim.cu:412-443)
+* a NaN similarity never wins; a query token whose similarities are all NaN
+  contributes -inf and argmax 0               (maxsim.cu `v > max`, test_nan_inf.py:33-92)
+* argmax slots beyond a pair's query length are 0 (maxsim.cu:543-547, 2005-2009)
+* backward routes g = dscore[pair] to dq[i] += g * d[j], dd[j] += g * q[i]
+  with j = argmax[pair, i], skipping j outside [0, Ld)
+                                              (reference.py:141-183, 186-229, 284-323)
+* gradients and scores are fp32              (torch_binding.h:83-85, 157-159)
+
+Inputs may be any float arrays (bf16/fp16 values should be passed already
+rounded to that precision, as the kernel sees them); all arithmetic is float64
+and results are rounded to fp32 at the end.
+
+How each function is pinned (tests/test_oracle.py): the known-answer cases
+of the reference's tests (single pair, all-identical rows -> argmax 0, pad
+garbage ignored, zero dscore, empty pair list), closed forms (score(q, q) =
+Lq for distinct unit rows), torch's own einsum + max(dim) and its autograd on
+finite inputs, NaN/inf contracts, cross-surface identities, and planted
+mistakes that those checks must catch.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "pair_forward",
+    "contrastive_forward",
+    "padded_forward",
+    "packed_forward",
+    "contrastive_backward",
+    "padded_backward",
+    "packed_backward",
+]
+
+
+def _as64(x) -> np.ndarray:
+    return np.asarray(x, dtype=np.float64)
+
+
+def _row_max_first(sim: np.ndarray):
+    """Per-row (max, first argmax) with NaN treated as never winning."""
+    clean = np.where(np.isnan(sim), -np.inf, sim)
+    idx = np.argmax(clean, axis=1) if clean.shape[1] else np.zeros(clean.shape[0], np.int64)
+    best = clean[np.arange(clean.shape[0]), idx]
+    return best, idx
+
+
+def pair_forward(q, d):
+    """One pair (reference.py:20-47): ``q [Lq, D]``, ``d [Ld, D]`` ->
+    (float score, int32 argmax [Lq])."""
+    q, d = _as64(q), _as64(d)
+    best, idx = _row_max_first(q @ d.T)
+    return float(np.float32(best.sum())), idx.astype(np.int32)
+
+
+def contrastive_forward(queries, documents, offsets):
+    """All pairs (reference.py:232-281): ``[Nq, Lq, D]`` x packed ``[T, D]``
+    with CSR ``offsets [Nb+1]`` -> (fp32 ``[Nq, Nb]``, int32 ``[Nq, Nb, Lq]``)."""
+    q = _as64(queries)
+    d = _as64(documents)
+    offs = np.asarray(offsets, dtype=np.int64)
+    Nq, Lq, D = q.shape
+    Nb = offs.size - 1
+    flat = q.reshape(Nq * Lq, D)
+    scores = np.empty((Nq, Nb), np.float64)
+    argmax = np.zeros((Nq, Nb, Lq), np.int32)
+    for b in range(Nb):
+        best, idx = _row_max_first(flat @ d[offs[b]:offs[b + 1]].T)
+        scores[:, b] = best.reshape(Nq, Lq).sum(axis=1)
+        argmax[:, b, :] = idx.reshape(Nq, Lq)
+    return scores.astype(np.float32), argmax
+
+
+def padded_forward(queries, documents, query_lengths, doc_lengths):
+    """Padded rerank (reference.py:112-138, 326-361): ``[B, Lq, D]`` x
+    ``[B, C, Ld, D]`` -> (fp32 ``[B, C]``, int32 ``[B, C, Lq]``).  Rows past
+    the lengths are never read; argmax slots past ``query_lengths[b]`` are 0."""
+    q = _as64(queries)
+    d = _as64(documents)
+    ql = np.asarray(query_lengths, dtype=np.int64)
+    dl = np.asarray(doc_lengths, dtype=np.int64)
+    B, Lq, _ = q.shape
+    C = d.shape[1]
+    scores = np.empty((B, C), np.float64)
+    argmax = np.zeros((B, C, Lq), np.int32)
+    for b in range(B):
+        qb = q[b, :ql[b]]
+        for c in range(C):
+            best, idx = _row_max_first(qb @ d[b, c, :dl[b, c]].T)
+            scores[b, c] = best.sum()
+            argmax[b, c, :ql[b]] = idx
+    return scores.astype(np.float32), argmax
+
+
+def packed_forward(queries, query_offsets, documents, document_offsets,
+                   pair_query_ids, pair_document_ids, max_q_len):
+    """Packed pairs (reference.py:50-109) -> (fp32 ``[P]``, int32 ``[P, max_q_len]``)."""
+    q = _as64(queries)
+    d = _as64(documents)
+    qo = np.asarray(query_offsets, dtype=np.int64)
+    do = np.asarray(document_offsets, dtype=np.int64)
+    qi = np.asarray(pair_query_ids, dtype=np.int64)
+    di = np.asarray(pair_document_ids, dtype=np.int64)
+    P = qi.size
+    scores = np.empty(P, np.float64)
+    argmax = np.zeros((P, max_q_len), np.int32)
+    for k in range(P):
+        qs, qe = qo[qi[k]], qo[qi[k] + 1]
+        best, idx = _row_max_first(q[qs:qe] @ d[do[di[k]]:do[di[k] + 1]].T)
+        scores[k] = best.sum()
+        argmax[k, :qe - qs] = idx
+    return scores.astype(np.float32), argmax
+
+
+def contrastive_backward(dscore, queries, documents, offsets, argmax):
+    """reference.py:284-323 -> (fp32 dq ``[Nq, Lq, D]``, fp32 dd ``[T, D]``)."""
+    g = _as64(dscore)
+    q = _as64(queries)
+    d = _as64(documents)
+    offs = np.asarray(offsets, dtype=np.int64)
+    am = np.asarray(argmax, dtype=np.int64)
+    Nq, Lq, D = q.shape
+    Nb = offs.size - 1
+    dq = np.zeros_like(q)
+    dd = np.zeros_like(d)
+    lens = (offs[1:] - offs[:-1])[None, :, None]
+    ok = (am >= 0) & (am < lens)
+    rows = offs[:-1][None, :, None] + np.where(ok, am, 0)
+    w = np.where(ok, g[:, :, None], 0.0)                       # [Nq, Nb, Lq]
+    dq += np.einsum("qbi,qbid->qid", w, d[rows])
+    np.add.at(dd, rows.reshape(-1), (w[..., None] * q[:, None, :, :]).reshape(-1, D))
+    return dq.astype(np.float32), dd.astype(np.float32)
+
+
+def padded_backward(dscore, queries, documents, query_lengths, doc_lengths, argmax):
+    """reference.py:141-183 -> (fp32 dq ``[B, Lq, D]``, fp32 dd ``[B, C, Ld, D]``)."""
+    g = _as64(dscore)
+    q = _as64(queries)
+    d = _as64(documents)
+    ql = np.asarray(query_lengths, dtype=np.int64)
+    dl = np.asarray(doc_lengths, dtype=np.int64)
+    am = np.asarray(argmax, dtype=np.int64)
+    B, C, Ld, D = d.shape
+    dq = np.zeros_like(q)
+    dd = np.zeros_like(d)
+    for b in range(B):
+        for c in range(C):
+            for i in range(ql[b]):
+                j = am[b, c, i]
+                if j < 0 or j >= dl[b, c]:
+                    continue
+                dq[b, i] += g[b, c] * d[b, c, j]
+                dd[b, c, j] += g[b, c] * q[b, i]
+    return dq.astype(np.float32), dd.astype(np.float32)
+
+
+def packed_backward(dscore, queries, query_offsets, documents, document_offsets,
+                    pair_query_ids, pair_document_ids, argmax):
+    """reference.py:186-229 -> (fp32 dq ``[Tq, D]``, fp32 dd ``[Td, D]``)."""
+    g = _as64(dscore)
+    q = _as64(queries)
+    d = _as64(documents)
+    qo = np.asarray(query_offsets, dtype=np.int64)
+    do = np.asarray(document_offsets, dtype=np.int64)
+    qi = np.asarray(pair_query_ids, dtype=np.int64)
+    di = np.asarray(pair_document_ids, dtype=np.int64)
+    am = np.asarray(argmax, dtype=np.int64)
+    dq = np.zeros_like(q)
+    dd = np.zeros_like(d)
+    for k in range(qi.size):
+        qs, qe = qo[qi[k]], qo[qi[k] + 1]
+        ds, de = do[di[k]], do[di[k] + 1]
+        j = am[k, :qe - qs]
+        ok = (j >= 0) & (j < de - ds)
+        rq = np.arange(qs, qe)[ok]
+        rd = ds + j[ok]
+        np.add.at(dq, rq, g[k] * d[rd])
+        np.add.at(dd, rd, g[k] * q[rq])
+    return dq.astype(np.float32), dd.astype(np.float32)

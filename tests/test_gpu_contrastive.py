@@ -1,0 +1,156 @@
+"""Contrastive surface on the GPU vs the CPU oracle (reference tests:
+tests/test_contrastive.py, test_edge_shapes.py:165-190, test_nan_inf.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import maxsim_amd
+from maxsim_amd._ops import ops
+from oracle import maxsim_oracle as oracle
+
+from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, check_argmax,
+                       make_contrastive, np64, npi)
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_forward(q, d, off, scores, argmax):
+    qn, dn, on = np64(q), np64(d), npi(off)
+    s_ref, a_ref = oracle.contrastive_forward(qn, dn, on)
+    assert scores.shape == s_ref.shape and scores.dtype == torch.float32
+    assert_close(scores, s_ref, **SCORE_TOL[q.dtype])
+    if argmax is not None:
+        assert argmax.dtype == torch.int32 and tuple(argmax.shape) == a_ref.shape
+        check_argmax(npi(argmax), a_ref,
+                     lambda idx: qn[idx[0], idx[2]],
+                     lambda idx, j: dn[on[idx[1]] + j])
+    return a_ref
+
+
+SHAPES = [
+    # Nq, Lq, dim, doc lengths
+    pytest.param(3, 16, 64, [37, 64, 200, 17, 81], id="ragged-Lq16-d64"),
+    pytest.param(5, 32, 128, [128, 300, 33, 1, 64, 512, 7], id="Lq32-d128"),
+    pytest.param(17, 32, 128, [40] * 9, id="Nq17-partial-group"),
+    pytest.param(2, 40, 128, [50, 90, 31], id="Lq40-two-blocks"),
+    pytest.param(2, 100, 64, [50, 90], id="Lq100-pair-kernel"),
+    pytest.param(1, 16, 16, [16], id="single"),
+    pytest.param(1, 16, 16, [1], id="Ld1"),
+    pytest.param(1, 16, 16, [17], id="Ld17"),
+    pytest.param(1, 16, 32, [16, 32, 48, 64], id="tile-boundaries"),
+    pytest.param(2, 16, 32, [7, 8, 100], id="mixed-ragged"),
+    pytest.param(1, 16, 96, [1], id="dim96"),
+    pytest.param(3, 8, 24, [5, 70], id="dim24"),
+    pytest.param(2, 7, 20, [9, 33], id="dim20-odd"),
+    pytest.param(2, 32, 256, [65, 129], id="dim256"),
+    pytest.param(1, 1, 128, [1000], id="Lq1-long-doc"),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("Nq,Lq,dim,d_lens", SHAPES)
+def test_contrastive_forward_and_argmax(Nq, Lq, dim, d_lens, dtype):
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=Nq * 131 + dim)
+    scores = maxsim_amd.score_contrastive(q, d, off)
+    _check_forward(q, d, off, scores, None)
+    scores2, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    _check_forward(q, d, off, scores2, argmax)
+    # score-only and with-argmax kernels agree bit for bit
+    assert torch.equal(scores, scores2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("Nq,Lq,dim,d_lens", SHAPES[:6] + SHAPES[11:14])
+def test_contrastive_backward(Nq, Lq, dim, d_lens, dtype):
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=7 + dim)
+    gen = torch.Generator().manual_seed(3)
+    dscore = torch.randn(Nq, len(d_lens), generator=gen).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq, dd = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    assert dq.dtype == torch.float32 and dd.dtype == torch.float32
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off), npi(argmax))
+    assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("d_lens", [[48, 48, 48], [47, 5, 33]])
+def test_contrastive_first_index_wins_on_ties(dtype, d_lens):
+    """All document rows identical -> every argmax is 0 (test_contrastive.py:70-95),
+    here for any Ld (no tile-size restriction: one MFMA path, no scalar tail)."""
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randn(2, 16, 32, generator=gen).to(dtype).to(DEVICE)
+    base = torch.randn(32, generator=gen).to(dtype)
+    d = base.expand(sum(d_lens), 32).contiguous().to(DEVICE)
+    off = torch.zeros(len(d_lens) + 1, dtype=torch.int32)
+    off[1:] = torch.tensor(d_lens).cumsum(0)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off.to(DEVICE))
+    assert torch.all(argmax == 0)
+
+
+def test_contrastive_duplicate_rows_pick_first_copy():
+    """Exact duplicates later in a document never win (C5's tie rule)."""
+    gen = torch.Generator().manual_seed(11)
+    lens = [300, 129, 64]
+    q = torch.nn.functional.normalize(torch.randn(4, 32, 128, generator=gen), dim=-1)
+    d = torch.nn.functional.normalize(torch.randn(sum(lens), 128, generator=gen), dim=-1)
+    off = torch.zeros(4, dtype=torch.int32)
+    off[1:] = torch.tensor(lens).cumsum(0)
+    # duplicate: every row j >= 100 of doc 0 copies row j - 100
+    d[100:300] = d[0:200].clone()
+    q, d, off = q.to(torch.bfloat16).to(DEVICE), d.to(torch.bfloat16).to(DEVICE), off.to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    assert int(argmax[:, 0].max()) < 100
+    _, a_ref = oracle.contrastive_forward(np64(q), np64(d), npi(off))
+    assert np.array_equal(npi(argmax)[:, 0], a_ref[:, 0])
+
+
+def test_contrastive_nan_gives_neg_inf():
+    """NaN in a query -> -inf for that query, finite elsewhere (test_nan_inf.py:33-92)."""
+    torch.manual_seed(0)
+    q = torch.randn(2, 16, 64, device=DEVICE, dtype=torch.float16)
+    d = torch.randn(3 * 32, 64, device=DEVICE, dtype=torch.float16)
+    cu = torch.arange(0, 4 * 32, 32, dtype=torch.int32, device=DEVICE)
+    q[1, 0, 0] = float("nan")
+    s = maxsim_amd.score_contrastive(q, d, cu)
+    assert torch.isinf(s[1]).all() and (s[1] < 0).all()
+    assert torch.isfinite(s[0]).all()
+    s2, a2 = maxsim_amd.score_contrastive_with_argmax(q, d, cu)
+    assert torch.equal(a2[1, :, 0], torch.zeros_like(a2[1, :, 0]))
+
+
+def test_contrastive_inf_propagates():
+    torch.manual_seed(1)
+    q = torch.randn(1, 16, 64, device=DEVICE, dtype=torch.float16)
+    d = torch.randn(2 * 32, 64, device=DEVICE, dtype=torch.float16).abs()
+    cu = torch.arange(0, 3 * 32, 32, dtype=torch.int32, device=DEVICE)
+    q[0, 0] = float("inf")
+    s = maxsim_amd.score_contrastive(q, d, cu)
+    assert torch.isinf(s).all() and (s > 0).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_contrastive_zero_dscore(dtype):
+    q, d, off = make_contrastive(1, 16, 32, [16, 16], dtype, seed=3)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq, dd = ops.maxsim_contrastive_backward(torch.zeros(1, 2, device=DEVICE), q, d, off, argmax)
+    assert torch.all(dq == 0) and torch.all(dd == 0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_contrastive_train_end_to_end(dtype):
+    q, d, off = make_contrastive(2, 16, 64, [40, 64, 20, 80], dtype, seed=4)
+    q.requires_grad_(True)
+    d.requires_grad_(True)
+    scores = maxsim_amd.score_contrastive_train(q, d, off)
+    w = torch.randn(2, 4, generator=torch.Generator().manual_seed(5)).to(DEVICE)
+    (scores * w).sum().backward()
+    s_ref, a_ref = oracle.contrastive_forward(np64(q), np64(d), npi(off))
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(w), np64(q), np64(d), npi(off), a_ref)
+    assert q.grad.dtype == dtype
+    tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    assert_close(q.grad, dq_ref, **tol)
+    assert_close(d.grad, dd_ref, **tol)

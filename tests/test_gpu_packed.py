@@ -1,0 +1,126 @@
+"""Packed surface on the GPU vs the CPU oracle (reference tests:
+tests/test_correctness.py, test_dtypes.py, test_ragged.py, test_packed_train.py,
+test_edge_shapes.py:118-154)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import maxsim_amd
+from maxsim_amd._ops import ops
+from oracle import maxsim_oracle as oracle
+
+from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, check_argmax,
+                       make_packed, np64, npi)
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # nq, nd, npairs, dim, q range, d range
+    pytest.param(6, 11, 17, 64, (4, 32), (8, 200), id="basic-d64"),
+    pytest.param(6, 11, 17, 96, (4, 32), (8, 200), id="d96"),
+    pytest.param(5, 7, 13, 64, (1, 1), (1, 1), id="len1"),
+    pytest.param(5, 7, 13, 64, (1, 64), (1, 64), id="ragged-short"),
+    pytest.param(5, 7, 13, 64, (4, 32), (16, 1024), id="long-docs"),
+    pytest.param(3, 4, 6, 128, (8, 24), (16, 96), id="train-shape"),
+    pytest.param(4, 9, 40, 128, (8, 100), (16, 300), id="Lq-up-to-100"),
+    pytest.param(2, 3, 5, 24, (3, 9), (5, 40), id="d24"),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("nq,nd,npairs,dim,qr,dr", CASES)
+def test_packed_forward_argmax_backward(nq, nd, npairs, dim, qr, dr, dtype):
+    q, qoff, d, doff, qids, dids = make_packed(nq, nd, npairs, dim, qr, dr, dtype, seed=npairs + dim)
+    qn, dn, qo, do = np64(q), np64(d), npi(qoff), npi(doff)
+    mql = int(np.diff(qo).max())
+    s_ref, a_ref = oracle.packed_forward(qn, qo, dn, do, npi(qids), npi(dids), mql)
+
+    s = maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids)
+    assert s.shape == (npairs,) and s.dtype == torch.float32
+    assert_close(s, s_ref, **SCORE_TOL[dtype])
+
+    s2, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    assert torch.equal(s, s2)
+    assert tuple(am.shape) == (npairs, mql)
+    qi, di = npi(qids), npi(dids)
+    check_argmax(npi(am), a_ref, lambda idx: qn[qo[qi[idx[0]]] + idx[1]],
+                 lambda idx, j: dn[do[di[idx[0]]] + j])
+
+    g = torch.randn(npairs, generator=torch.Generator().manual_seed(5)).to(DEVICE)
+    dq, dd = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, mql)
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), qn, qo, dn, do, qi, di, npi(am))
+    assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+
+
+def test_packed_single_pair_single_token_closed_form():
+    """test_correctness.py:39-50: 1 x 1 tokens -> score is the dot product."""
+    q = torch.randn(1, 16, device=DEVICE)
+    d = torch.randn(1, 16, device=DEVICE)
+    one = torch.tensor([0, 1], dtype=torch.int32, device=DEVICE)
+    z = torch.tensor([0], dtype=torch.int32, device=DEVICE)
+    s = maxsim_amd.score_pairs_packed(q, one, d, one, z, z)
+    expected = float(np.dot(np64(q)[0], np64(d)[0]))
+    assert abs(float(s[0]) - expected) <= 1e-5 * max(1.0, abs(expected))
+
+
+def test_packed_empty_pairs():
+    q, qoff, d, doff, qids, dids = make_packed(2, 3, 0, 32, (2, 8), (2, 16), torch.float32, seed=0)
+    s = maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids)
+    assert s.shape == (0,) and s.dtype == torch.float32
+
+
+def test_packed_max_q_len_larger_than_needed():
+    q, qoff, d, doff, qids, dids = make_packed(3, 4, 6, 64, (8, 24), (16, 96), torch.bfloat16, seed=2)
+    s, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids, max_q_len=40)
+    assert am.shape == (6, 40)
+    qo = npi(qoff)
+    lens = np.diff(qo)[npi(qids)]
+    for k in range(6):
+        assert np.all(npi(am)[k, lens[k]:] == 0)
+
+
+def test_packed_nan_gives_neg_inf():
+    Lq, Ld, D = 16, 32, 64
+    q = torch.randn(2 * Lq, D, device=DEVICE, dtype=torch.float16)
+    d = torch.randn(3 * Ld, D, device=DEVICE, dtype=torch.float16)
+    qoff = torch.arange(0, 3 * Lq, Lq, dtype=torch.int32, device=DEVICE)
+    doff = torch.arange(0, 4 * Ld, Ld, dtype=torch.int32, device=DEVICE)
+    qids = torch.tensor([0, 1], dtype=torch.int32, device=DEVICE)
+    dids = torch.tensor([0, 0], dtype=torch.int32, device=DEVICE)
+    q[Lq] = float("nan")
+    s = maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids, max_q_len=Lq)
+    assert torch.isfinite(s[0]) and torch.isinf(s[1]) and s[1] < 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_packed_ties_first_index(dtype):
+    base = torch.randn(32, dtype=dtype)
+    d = base.expand(47, 32).contiguous().to(DEVICE)
+    q = torch.randn(12, 32, dtype=dtype, device=DEVICE)
+    qo = torch.tensor([0, 12], dtype=torch.int32, device=DEVICE)
+    do = torch.tensor([0, 47], dtype=torch.int32, device=DEVICE)
+    z = torch.zeros(1, dtype=torch.int32, device=DEVICE)
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qo, d, do, z, z)
+    assert torch.all(am == 0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_packed_train_end_to_end(dtype):
+    q, qoff, d, doff, qids, dids = make_packed(3, 4, 6, 64, (8, 24), (16, 96), dtype, seed=2)
+    q.requires_grad_(True)
+    d.requires_grad_(True)
+    s = maxsim_amd.score_pairs_packed_train(q, qoff, d, doff, qids, dids)
+    w = torch.randn(6, generator=torch.Generator().manual_seed(1)).to(DEVICE)
+    (s * w).sum().backward()
+    qo, do = npi(qoff), npi(doff)
+    mql = int(np.diff(qo).max())
+    _, a_ref = oracle.packed_forward(np64(q), qo, np64(d), do, npi(qids), npi(dids), mql)
+    dq_ref, dd_ref = oracle.packed_backward(np64(w), np64(q), qo, np64(d), do, npi(qids),
+                                            npi(dids), a_ref)
+    tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    assert_close(q.grad, dq_ref, **tol)
+    assert_close(d.grad, dd_ref, **tol)

@@ -1,0 +1,127 @@
+"""Padded surface on the GPU vs the CPU oracle (reference tests:
+tests/test_padded.py, test_argmax.py, test_backward.py, test_edge_shapes.py:37-110)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import maxsim_amd
+from maxsim_amd._ops import ops
+from oracle import maxsim_oracle as oracle
+
+from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, check_argmax,
+                       make_padded, np64, npi)
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # B, C, Lq, Ld, dim, full lengths?
+    pytest.param(4, 5, 32, 128, 64, False, id="random-lengths"),
+    pytest.param(1, 1, 1, 1, 16, True, id="smallest"),
+    pytest.param(1, 1, 16, 17, 16, True, id="Ld17"),
+    pytest.param(1, 1, 16, 65, 16, True, id="Ld65"),
+    pytest.param(2, 2, 8, 24, 24, True, id="dim24"),
+    pytest.param(1, 1, 32, 100, 96, True, id="dim96"),
+    pytest.param(4, 1, 16, 32, 64, True, id="C1"),
+    pytest.param(1, 8, 16, 32, 64, True, id="B1"),
+    pytest.param(3, 4, 64, 50, 128, False, id="Lq64"),
+    pytest.param(2, 3, 130, 40, 32, False, id="Lq130-three-block-groups"),
+    pytest.param(2, 2, 32, 300, 128, False, id="Ld300"),
+]
+
+
+def _full_or_random(B, C, Lq, Ld, full):
+    if full:
+        return torch.full((B,), Lq, dtype=torch.int32), torch.full((B, C), Ld, dtype=torch.int32)
+    return None, None
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("B,C,Lq,Ld,dim,full", SHAPES)
+def test_padded_forward_argmax_backward(B, C, Lq, Ld, dim, full, dtype):
+    ql, dl = _full_or_random(B, C, Lq, Ld, full)
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, dim, dtype, seed=B * 7 + Ld, qlen=ql, dlen=dl)
+    qn, dn = np64(q), np64(d)
+    s_ref, a_ref = oracle.padded_forward(qn, dn, npi(qlen), npi(dlen))
+
+    s = maxsim_amd.score_candidates_padded(q, d, qlen, dlen)
+    assert s.shape == (B, C) and s.dtype == torch.float32
+    assert_close(s, s_ref, **SCORE_TOL[dtype])
+
+    s2, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    assert torch.equal(s, s2)
+    assert tuple(am.shape) == (B, C, Lq) and am.dtype == torch.int32
+    check_argmax(npi(am), a_ref, lambda idx: qn[idx[0], idx[2]],
+                 lambda idx, j: dn[idx[0], idx[1], j])
+    # pad slots are 0
+    qlc = npi(qlen)
+    for b in range(B):
+        assert np.all(npi(am)[b, :, qlc[b]:] == 0)
+
+    g = torch.randn(B, C, generator=torch.Generator().manual_seed(9)).to(DEVICE)
+    dq, dd = ops.maxsim_padded_backward(
+        g.reshape(-1).contiguous(), q.reshape(B * Lq, dim).contiguous(),
+        d.reshape(B * C * Ld, dim).contiguous(), qlen, dlen.reshape(-1).contiguous(),
+        am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
+    dq_ref, dd_ref = oracle.padded_backward(np64(g), qn, dn, npi(qlen), npi(dlen), npi(am))
+    assert_close(dq.view(B, Lq, dim), dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd.view(B, C, Ld, dim), dd_ref, **GRAD_TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_padded_ignores_pad_positions(dtype):
+    """Garbage -- even NaN -- past the declared lengths never changes results
+    (test_padded.py:38-61)."""
+    B, C, Lq, Ld, D = 2, 3, 8, 40, 32
+    q, d, _, _ = make_padded(B, C, Lq, Ld, D, dtype, seed=1)
+    qlen = torch.tensor([4, 6], dtype=torch.int32, device=DEVICE)
+    dlen = torch.tensor([[10, 8, 4], [40, 1, 33]], dtype=torch.int32, device=DEVICE)
+    base_s, base_a = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    qc, dc = q.clone(), d.clone()
+    qc[0, 4:] = 1e4
+    qc[1, 6:] = float("nan")
+    dc[0, 0, 10:] = 1e4
+    dc[1, 1, 1:] = float("nan")
+    dc[1, 2, 33:] = -1e4
+    s, a = maxsim_amd.score_candidates_padded_with_argmax(qc, dc, qlen, dlen)
+    assert torch.equal(s, base_s) and torch.equal(a, base_a)
+
+
+def test_padded_first_index_wins_on_ties():
+    base = torch.randn(16, dtype=torch.float16)
+    d = base.view(1, 1, 1, 16).expand(1, 1, 37, 16).contiguous().to(DEVICE)
+    q = torch.randn(1, 16, 16, dtype=torch.float16, device=DEVICE)
+    _, a = maxsim_amd.score_candidates_padded_with_argmax(
+        q, d, torch.tensor([16], dtype=torch.int32, device=DEVICE),
+        torch.tensor([[37]], dtype=torch.int32, device=DEVICE))
+    assert torch.all(a == 0)
+
+
+def test_padded_nan_gives_neg_inf():
+    torch.manual_seed(0)
+    q = torch.randn(2, 16, 64, device=DEVICE, dtype=torch.float16)
+    d = torch.randn(2, 3, 32, 64, device=DEVICE, dtype=torch.float16)
+    qlen = torch.full((2,), 16, dtype=torch.int32, device=DEVICE)
+    dlen = torch.full((2, 3), 32, dtype=torch.int32, device=DEVICE)
+    q[1, 0, 0] = float("nan")
+    s = maxsim_amd.score_candidates_padded(q, d, qlen, dlen)
+    assert torch.isinf(s[1]).all() and (s[1] < 0).all()
+    assert torch.isfinite(s[0]).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+def test_padded_train_end_to_end(dtype):
+    B, C, Lq, Ld, D = 2, 4, 16, 32, 64
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, D, dtype, seed=2)
+    q.requires_grad_(True)
+    d.requires_grad_(True)
+    scores = maxsim_amd.score_candidates_padded_train(q, d, qlen, dlen)
+    w = torch.randn(B, C, generator=torch.Generator().manual_seed(4)).to(DEVICE)
+    (scores * w).sum().backward()
+    _, a_ref = oracle.padded_forward(np64(q), np64(d), npi(qlen), npi(dlen))
+    dq_ref, dd_ref = oracle.padded_backward(np64(w), np64(q), np64(d), npi(qlen), npi(dlen), a_ref)
+    tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    assert_close(q.grad, dq_ref, **tol)
+    assert_close(d.grad, dd_ref, **tol)
