@@ -23,6 +23,8 @@
 #include "maxsim_common.h"
 #include "maxsim_host.h"
 
+#include <algorithm>
+
 namespace maxsim {
 
 // 8 consecutive elements of a row as fp32 (elements at k >= dim read 0).
@@ -207,16 +209,22 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 }
 
 // ---------------------------------------------------------------------------
-// dd, contrastive: workgroup per (document, row chunk), LDS accumulation.
-// LDS row layout: element d of a row lives at (d % 8) * nslices + d / 8, so
-// the 16..32 lanes that add one 8-element slice each hit consecutive words.
+// dd, contrastive: one workgroup per document, LDS counting sort.
+//
+// Document b receives one entry per (query q, token i): row argmax[q, b, i].
+// The workgroup buckets those entries by target row in LDS (histogram,
+// exclusive scan, scatter of entry ids), then 16-lane groups each own one row
+// at a time and sum g[q, b] * q_row over the row's bucket in fp32 registers,
+// writing the gradient row once.  No floating-point atomics; every row of the
+// document is written (zeros for rows no entry points at).  Documents longer
+// than `rows_per_pass` rows and entry sets larger than `entries_per_pass` are
+// processed in passes (later entry passes add to the rows already written).
 // ---------------------------------------------------------------------------
 struct DdArgs {
   const float* dscore;
   const void* q;
   const int32_t* argmax;
   const int32_t* doff;
-  const int32_t* chunk_doc;   // unused: chunks are found by search below
   float* dd;
   int64_t nq;
   int64_t nb;
@@ -224,99 +232,146 @@ struct DdArgs {
   int lq;
   int dim;
   int nslices;
-  int rows_per_chunk;
-  int lanes_per_entry;   // power of two >= nslices, <= 64
-  int row_stride;        // floats per LDS row
-  int64_t chunks_total;
+  int rows_per_pass;     // R: rows bucketed per pass (LDS: 2 * (R + 1) ints)
+  int entries_per_pass;  // E: entry ids held per pass (LDS: E ints)
 };
 
-constexpr int kDdThreads = 256;
-constexpr int kDdList = 256;  // entries compacted per round (one per thread)
+constexpr int kDdThreads = 512;
+constexpr int kDdGroup = 16;                        // lanes per row
+constexpr int kDdGroups = kDdThreads / kDdGroup;    // rows in flight per workgroup
+constexpr int kDdMaxSlices = MAXSIM_AMD_MAX_DIM / 8 / kDdGroup;  // per lane
 
 template <typename T>
 __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a,
                                                                     bool vec) {
   using S = typename T::storage;
-  extern __shared__ float smem[];
-  float* acc = smem;                                            // rows * stride
-  int* list = reinterpret_cast<int*>(smem + a.rows_per_chunk * a.row_stride);
-  int* list_j = list + kDdList;
-  int* counter = list_j + kDdList;
+  extern __shared__ int lds_i[];
+  const int R = a.rows_per_pass;
+  int* start = lds_i;                 // [R + 1]
+  int* cursor = start + (R + 1);      // [R + 1]
+  int* ids = cursor + (R + 1);        // [E]
 
-  // Map blockIdx.x -> (doc b, chunk k) by walking the offsets: chunk index
-  // of doc b starts at sum_{b' < b} ceil(Ld_b' / R).  A binary search over
-  // docs needs that prefix, so each block computes it with a linear scan of
-  // ceil(Ld/R) (cheap: Nb reads of the offsets, cached in L2).
-  const int64_t cid = blockIdx.x;
-  int64_t b = -1, k = 0, seen = 0;
-  for (int64_t bb = 0; bb < a.nb; ++bb) {
-    const int64_t s = a.doff[bb], e = a.doff[bb + 1];
-    const int64_t ld = (s >= 0 && e > s && e <= a.total_d) ? (e - s) : 0;
-    const int64_t nch = (ld + a.rows_per_chunk - 1) / a.rows_per_chunk;
-    if (cid < seen + nch) {
-      b = bb;
-      k = cid - seen;
-      break;
-    }
-    seen += nch;
-  }
-  if (b < 0) return;
-  const int64_t d0 = a.doff[b];
-  const int ld = a.doff[b + 1] - (int)d0;
-  const int r0 = (int)(k * a.rows_per_chunk);
-  const int nrows = min(a.rows_per_chunk, ld - r0);
-
+  const int64_t b = blockIdx.x;
+  const int64_t d0 = a.doff[b], d1 = a.doff[b + 1];
+  if (d0 < 0 || d1 <= d0 || d1 > a.total_d) return;
+  const int ld = (int)(d1 - d0);
   const int tid = threadIdx.x;
-  for (int x = tid; x < nrows * a.row_stride; x += kDdThreads) acc[x] = 0.0f;
-
+  const int lane = tid & 63;
+  const int grp = tid / kDdGroup;
+  const int gl = tid % kDdGroup;
   const S* __restrict__ Q = static_cast<const S*>(a.q);
   const int64_t n_entries = a.nq * a.lq;
-  const int lpe = a.lanes_per_entry;
-  const int groups = kDdThreads / lpe;
-  const int grp = tid / lpe;
-  const int gl = tid - grp * lpe;
+  const int32_t* am_b = a.argmax + b * a.lq;   // entry (q, i) at am_b[q*nb*lq + i]
+  const int64_t am_qstride = a.nb * a.lq;
 
-  for (int64_t e0 = 0; e0 < n_entries; e0 += kDdList) {
-    if (tid == 0) *counter = 0;
-    __syncthreads();
-    const int64_t e = e0 + tid;
-    if (e < n_entries) {
-      const int64_t qq = e / a.lq;
-      const int i = (int)(e - qq * a.lq);
-      const int j = a.argmax[(qq * a.nb + b) * a.lq + i];
-      if (j >= r0 && j < r0 + nrows) {
-        const int slot = atomicAdd(counter, 1);
-        list[slot] = (int)(e - e0);
-        list_j[slot] = j - r0;
+  for (int r0 = 0; r0 < ld; r0 += R) {
+    const int nrows = min(R, ld - r0);
+    for (int64_t e0 = 0; e0 < n_entries; e0 += a.entries_per_pass) {
+      const int ne = (int)min((int64_t)a.entries_per_pass, n_entries - e0);
+      for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
+      __syncthreads();
+      // 1. histogram of target rows
+      for (int x = tid; x < ne; x += kDdThreads) {
+        const int64_t e = e0 + x;
+        const int64_t qq = e / a.lq;
+        const int j = am_b[qq * am_qstride + (e - qq * a.lq)] - r0;
+        if (j >= 0 && j < nrows) atomicAdd(&start[j + 1], 1);
       }
-    }
-    __syncthreads();
-    const int cnt = *counter;
-    for (int x = grp; x < cnt; x += groups) {
-      const int64_t e2 = e0 + list[x];
-      const int jr = list_j[x];
-      const int64_t qq = e2 / a.lq;
-      const float g = a.dscore[qq * a.nb + b];
-      for (int sl = gl; sl < a.nslices; sl += lpe) {
-        float v[8];
-        load8f<T>(Q + e2 * (int64_t)a.dim, sl * 8, a.dim, vec, v);
-        float* dst = acc + jr * a.row_stride + sl;
+      __syncthreads();
+      // 2. inclusive scan of start[1..nrows] by wave 0 (lane owns a run)
+      if (tid < 64) {
+        const int per = (nrows + 63) / 64;
+        const int lo = 1 + lane * per;
+        const int hi = min(lo + per, nrows + 1);
+        int run = 0;
+        for (int x = lo; x < hi; ++x) run += start[x];
+        int incl = run;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (sl * 8 + u < a.dim) atomicAdd(dst + u * a.nslices, g * v[u]);
+        for (int off = 1; off < 64; off <<= 1) {
+          const int v = __shfl_up(incl, off);
+          if (lane >= off) incl += v;
+        }
+        int acc = incl - run;
+        for (int x = lo; x < hi; ++x) {
+          acc += start[x];
+          start[x] = acc;
+        }
       }
-    }
-    __syncthreads();
-  }
-
-  // Write the chunk once.
-  for (int x = tid; x < nrows * a.nslices; x += kDdThreads) {
-    const int r = x / a.nslices;
-    const int sl = x - r * a.nslices;
-    float v[8];
+      __syncthreads();
+      for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
+      __syncthreads();
+      // 3. scatter entry ids into their row buckets
+      for (int x = tid; x < ne; x += kDdThreads) {
+        const int64_t e = e0 + x;
+        const int64_t qq = e / a.lq;
+        const int j = am_b[qq * am_qstride + (e - qq * a.lq)] - r0;
+        if (j >= 0 && j < nrows) ids[atomicAdd(&cursor[j], 1)] = x;
+      }
+      __syncthreads();
+      // 4. per-row fp32 sums, one 16-lane group per row
+      for (int rr = grp; rr < nrows; rr += kDdGroups) {
+        float acc[kDdMaxSlices][8];
+        float* dst = a.dd + (d0 + r0 + rr) * (int64_t)a.dim;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = acc[r * a.row_stride + sl + u * a.nslices];
-    store8f(a.dd + (d0 + r0 + r) * (int64_t)a.dim, sl * 8, a.dim, vec, v);
+        for (int u = 0; u < kDdMaxSlices; ++u) {
+          const int sl = gl + u * kDdGroup;
+          if (sl < a.nslices && e0 > 0) {
+            if (vec) {
+              const float4 x0 = *reinterpret_cast<const float4*>(dst + sl * 8);
+              const float4 x1 = *reinterpret_cast<const float4*>(dst + sl * 8 + 4);
+              acc[u][0] = x0.x; acc[u][1] = x0.y; acc[u][2] = x0.z; acc[u][3] = x0.w;
+              acc[u][4] = x1.x; acc[u][5] = x1.y; acc[u][6] = x1.z; acc[u][7] = x1.w;
+            } else {
+#pragma unroll
+              for (int k = 0; k < 8; ++k)
+                acc[u][k] = (sl * 8 + k < a.dim) ? dst[sl * 8 + k] : 0.0f;
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[u][k] = 0.0f;
+          }
+        }
+        const int s_end = start[rr + 1];
+        int s = start[rr];
+        // two entries per step keeps two row loads in flight per lane
+        for (; s + 1 < s_end; s += 2) {
+          const int64_t ea = e0 + ids[s], eb = e0 + ids[s + 1];
+          const float ga = a.dscore[(ea / a.lq) * a.nb + b];
+          const float gb = a.dscore[(eb / a.lq) * a.nb + b];
+#pragma unroll
+          for (int u = 0; u < kDdMaxSlices; ++u) {
+            const int sl = gl + u * kDdGroup;
+            if (sl < a.nslices) {
+              float va[8], vb[8];
+              load8f<T>(Q + ea * (int64_t)a.dim, sl * 8, a.dim, vec, va);
+              load8f<T>(Q + eb * (int64_t)a.dim, sl * 8, a.dim, vec, vb);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc[u][k] = fmaf(gb, vb[k], fmaf(ga, va[k], acc[u][k]));
+            }
+          }
+        }
+        if (s < s_end) {
+          const int64_t ea = e0 + ids[s];
+          const float ga = a.dscore[(ea / a.lq) * a.nb + b];
+#pragma unroll
+          for (int u = 0; u < kDdMaxSlices; ++u) {
+            const int sl = gl + u * kDdGroup;
+            if (sl < a.nslices) {
+              float va[8];
+              load8f<T>(Q + ea * (int64_t)a.dim, sl * 8, a.dim, vec, va);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc[u][k] = fmaf(ga, va[k], acc[u][k]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kDdMaxSlices; ++u) {
+          const int sl = gl + u * kDdGroup;
+          if (sl < a.nslices) store8f(dst, sl * 8, a.dim, vec, acc[u]);
+        }
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -469,12 +524,19 @@ static void launch_dq(const DqArgs& a, bool vec, hipStream_t st) {
 }
 
 template <typename T>
-static void launch_dd_contrastive(DdArgs a, const int32_t* /*unused*/, bool vec,
-                                  int64_t nchunks, hipStream_t st) {
-  const size_t lds = (size_t)a.rows_per_chunk * a.row_stride * sizeof(float) +
-                     (2 * kDdList + 1) * sizeof(int);
-  hipLaunchKernelGGL(dd_contrastive_kernel<T>, dim3((unsigned)nchunks),
-                     dim3(kDdThreads), lds, st, a, vec);
+static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL(dd_contrastive_kernel<T>, dim3((unsigned)a.nb), dim3(kDdThreads), lds,
+                     st, a, vec);
+}
+
+// Largest dynamic LDS allocation one workgroup may use on this device.
+static size_t max_lds_per_block() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 64 * 1024;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      v <= 0)
+    return 64 * 1024;
+  return (size_t)v;
 }
 
 template <typename T>
@@ -554,11 +616,10 @@ int maxsim_amd_contrastive_backward(
   MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, st);
   if (int e = check_launch("dq_gather_kernel")) return e;
 
-  // dd: rows of documents with invalid offsets, and tokens not covered by any
-  // document, are not owned by any chunk; zero the whole buffer first only
-  // when the offsets do not tile [0, total_d_tokens) -- the caller's layout
-  // is validated upstream, so the fast path assumes they do and the kernel
-  // writes every row of every valid document.
+  // dd: one workgroup per document; every row of every valid document is
+  // written.  LDS holds the row buckets (2 * (R + 1) ints) and up to E entry
+  // ids; use up to 80 KB when the device allows, so C5-sized batches
+  // (Nq * Lq = 16384 entries) need a single pass.
   DdArgs da{};
   da.dscore = dscore;
   da.q = queries;
@@ -571,17 +632,23 @@ int maxsim_amd_contrastive_backward(
   da.lq = (int)Lq;
   da.dim = (int)dim;
   da.nslices = nslices;
-  da.lanes_per_entry = pow2_at_least(nslices < 64 ? nslices : 64);
-  da.row_stride = nslices * 8 + 4;
-  int rows = (int)((60 * 1024 - (2 * kDdList + 1) * 4) / (da.row_stride * 4));
-  if (rows > 256) rows = 256;
-  da.rows_per_chunk = rows;
-  // Upper bound on the number of chunks without reading the offsets on the
-  // host: sum ceil(Ld/R) <= total/R + Nb.  Surplus blocks find no chunk and
-  // exit immediately.
-  const int64_t nchunks = total_d_tokens / rows + num_documents;
-  da.chunks_total = nchunks;
-  MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, nullptr, vec, nchunks, st);
+  const size_t lds_cap = std::min<size_t>(max_lds_per_block(), 80 * 1024);
+  da.rows_per_pass = 1024;
+  const size_t bucket_bytes = 2 * (size_t)(da.rows_per_pass + 1) * sizeof(int);
+  int64_t e_cap = (int64_t)((lds_cap - bucket_bytes) / sizeof(int));
+  if (e_cap > 16384) e_cap = 16384;
+  da.entries_per_pass = (int)std::min<int64_t>(e_cap, std::max<int64_t>(num_queries * Lq, 1));
+  const size_t lds = bucket_bytes + (size_t)da.entries_per_pass * sizeof(int);
+  if (lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<BF16>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<F16>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<F32>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    (void)hipGetLastError();
+  }
+  MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, st);
   return check_launch("dd_contrastive_kernel");
 }
 

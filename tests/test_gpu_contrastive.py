@@ -99,8 +99,9 @@ def test_contrastive_duplicate_rows_pick_first_copy():
     d = torch.nn.functional.normalize(torch.randn(sum(lens), 128, generator=gen), dim=-1)
     off = torch.zeros(4, dtype=torch.int32)
     off[1:] = torch.tensor(lens).cumsum(0)
-    # duplicate: every row j >= 100 of doc 0 copies row j - 100
-    d[100:300] = d[0:200].clone()
+    # duplicate: rows 100..299 of doc 0 are copies of rows 0..99
+    d[100:200] = d[0:100]
+    d[200:300] = d[0:100]
     q, d, off = q.to(torch.bfloat16).to(DEVICE), d.to(torch.bfloat16).to(DEVICE), off.to(DEVICE)
     _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
     assert int(argmax[:, 0].max()) < 100
