@@ -50,6 +50,18 @@ def _as64(x) -> np.ndarray:
     return np.asarray(x, dtype=np.float64)
 
 
+def _sim(q: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """q @ d.T in float64 such that bitwise-identical document rows get
+    bitwise-identical similarities.  A BLAS gemm does not promise that (rows
+    that land in different micro-kernel tiles are summed in different
+    orders), and exact ties must be broken by index, so the rows are
+    de-duplicated first and the products mapped back."""
+    if d.shape[0] == 0:
+        return np.zeros((q.shape[0], 0))
+    uniq, inv = np.unique(d, axis=0, return_inverse=True)
+    return (q @ uniq.T)[:, inv.reshape(-1)]
+
+
 def _row_max_first(sim: np.ndarray):
     """Per-row (max, first argmax) with NaN treated as never winning."""
     clean = np.where(np.isnan(sim), -np.inf, sim)
@@ -62,7 +74,7 @@ def pair_forward(q, d):
     """One pair (reference.py:20-47): ``q [Lq, D]``, ``d [Ld, D]`` ->
     (float score, int32 argmax [Lq])."""
     q, d = _as64(q), _as64(d)
-    best, idx = _row_max_first(q @ d.T)
+    best, idx = _row_max_first(_sim(q, d))
     return float(np.float32(best.sum())), idx.astype(np.int32)
 
 
@@ -78,7 +90,7 @@ def contrastive_forward(queries, documents, offsets):
     scores = np.empty((Nq, Nb), np.float64)
     argmax = np.zeros((Nq, Nb, Lq), np.int32)
     for b in range(Nb):
-        best, idx = _row_max_first(flat @ d[offs[b]:offs[b + 1]].T)
+        best, idx = _row_max_first(_sim(flat, d[offs[b]:offs[b + 1]]))
         scores[:, b] = best.reshape(Nq, Lq).sum(axis=1)
         argmax[:, b, :] = idx.reshape(Nq, Lq)
     return scores.astype(np.float32), argmax
@@ -99,7 +111,7 @@ def padded_forward(queries, documents, query_lengths, doc_lengths):
     for b in range(B):
         qb = q[b, :ql[b]]
         for c in range(C):
-            best, idx = _row_max_first(qb @ d[b, c, :dl[b, c]].T)
+            best, idx = _row_max_first(_sim(qb, d[b, c, :dl[b, c]]))
             scores[b, c] = best.sum()
             argmax[b, c, :ql[b]] = idx
     return scores.astype(np.float32), argmax
@@ -119,7 +131,7 @@ def packed_forward(queries, query_offsets, documents, document_offsets,
     argmax = np.zeros((P, max_q_len), np.int32)
     for k in range(P):
         qs, qe = qo[qi[k]], qo[qi[k] + 1]
-        best, idx = _row_max_first(q[qs:qe] @ d[do[di[k]]:do[di[k] + 1]].T)
+        best, idx = _row_max_first(_sim(q[qs:qe], d[do[di[k]]:do[di[k] + 1]]))
         scores[k] = best.sum()
         argmax[k, :qe - qs] = idx
     return scores.astype(np.float32), argmax

@@ -1,0 +1,116 @@
+"""The C ABI library (CPU only: loading and argument checking, no kernels).
+
+Checks that libmaxsim_amd.so loads with ctypes, exports every function that
+include/maxsim_amd.h declares, and rejects bad arguments with the documented
+status codes before touching the GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "maxsim_amd.h"
+LIB = ROOT / "maxsim_amd" / "libmaxsim_amd.so"
+
+OK, INVALID, UNSUPPORTED = 0, 1, 2
+F32, F16, BF16 = 0, 1, 2
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(maxsim_amd_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built; run python -m maxsim_amd._build")
+    handle = ctypes.CDLL(str(LIB))
+    handle.maxsim_amd_last_error.restype = ctypes.c_char_p
+    return handle
+
+
+def test_header_declares_the_nine_ops_plus_helpers():
+    names = declared_functions()
+    assert len(names) == 11, names
+    for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
+               "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
+               "contrastive_forward_with_argmax", "contrastive_backward"]:
+        assert f"maxsim_amd_{op}" in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_abi_version(lib):
+    assert lib.maxsim_amd_abi_version() == 1
+
+
+I64 = ctypes.c_int64
+P = ctypes.c_void_p
+
+
+def _contrastive(lib, dtype=BF16, nq=2, lq=16, total=64, nb=2, dim=64, ptr=1, argmax=True):
+    fn = lib.maxsim_amd_contrastive_forward_with_argmax
+    fn.argtypes = [ctypes.c_int, P, I64, I64, P, I64, P, I64, I64, P, P, P]
+    p = P(ptr) if ptr else None
+    return fn(dtype, p, nq, lq, p, total, p, nb, dim, p, p if argmax else None, None)
+
+
+def test_rejects_unknown_dtype(lib):
+    assert _contrastive(lib, dtype=7) == INVALID
+    assert b"dtype" in lib.maxsim_amd_last_error()
+
+
+def test_rejects_bad_dims(lib):
+    assert _contrastive(lib, dim=0) == INVALID
+    assert b"dim" in lib.maxsim_amd_last_error()
+    assert _contrastive(lib, dim=4096) == UNSUPPORTED
+    assert b"256" in lib.maxsim_amd_last_error()
+
+
+def test_rejects_nonpositive_lq_and_negative_sizes(lib):
+    assert _contrastive(lib, lq=0) == INVALID
+    assert b"Lq" in lib.maxsim_amd_last_error()
+    assert _contrastive(lib, nq=-1) == INVALID
+
+
+def test_rejects_null_pointers(lib):
+    assert _contrastive(lib, ptr=0) == INVALID
+    assert b"null" in lib.maxsim_amd_last_error()
+
+
+def test_empty_problem_is_a_noop(lib):
+    # zero queries: nothing to do, no device work, success
+    assert _contrastive(lib, nq=0, ptr=0) == OK
+    assert lib.maxsim_amd_last_error() == b""
+
+
+def test_packed_rejects_bad_max_q_len(lib):
+    fn = lib.maxsim_amd_packed_forward_with_argmax
+    fn.argtypes = [ctypes.c_int, P, I64, P, I64, P, I64, P, I64, P, P, I64, I64, I64, P, P, P]
+    one = P(1)
+    assert fn(F32, one, 4, one, 1, one, 4, one, 1, one, one, 1, 8, 0, one, one, None) == INVALID
+    assert b"max_q_len" in lib.maxsim_amd_last_error()
+
+
+def test_padded_rejects_bad_extents(lib):
+    fn = lib.maxsim_amd_padded_forward_with_argmax
+    fn.argtypes = [ctypes.c_int, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]
+    one = P(1)
+    assert fn(F16, one, one, one, one, 2, 3, 0, 8, 64, one, one, None) == INVALID
+    assert fn(F16, one, one, one, one, 2, -3, 4, 8, 64, one, one, None) == INVALID
+
+
+def test_backward_rejects_null_grads(lib):
+    fn = lib.maxsim_amd_padded_backward
+    fn.argtypes = [ctypes.c_int, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]
+    one = P(1)
+    assert fn(BF16, one, one, one, one, one, one, 2, 3, 4, 8, 64, None, one, None) == INVALID
+    assert b"null" in lib.maxsim_amd_last_error()
