@@ -135,6 +135,11 @@ __device__ __forceinline__ void mask_rows(f32x16& acc, int h, int valid) {
 // reference kernels, maxsim.cu:412-443): ascending document order, strict
 // `>` so the first index wins ties, NaN never wins (fmaxf ignores NaN and
 // `>`/`==` are false for NaN).  `row_base` is tile_row0 + 4*h.
+//
+// Cost: a max3 tree (8 VALU) per tile; only when the tile beats the running
+// max, the first register equal to the tile max is located.  The sixteen
+// equality tests are independent (no compare -> select hazard chain) and the
+// selected constant is the register's row offset 8*(r>>2) + (r&3).
 template <bool ARGMAX>
 __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
                                             int& am, int row_base) {
@@ -149,10 +154,13 @@ __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
   if (tmax > m) {
     m = tmax;
     if constexpr (ARGMAX) {
-      int idx = 15;
+      bool eq[16];
 #pragma unroll
-      for (int r = 14; r >= 0; --r) idx = (acc[r] == tmax) ? r : idx;
-      am = row_base + 8 * (idx >> 2) + (idx & 3);
+      for (int r = 0; r < 16; ++r) eq[r] = acc[r] == tmax;
+      int off = 8 * (15 >> 2) + (15 & 3);
+#pragma unroll
+      for (int r = 14; r >= 0; --r) off = eq[r] ? (8 * (r >> 2) + (r & 3)) : off;
+      am = row_base + off;
     }
   }
 }

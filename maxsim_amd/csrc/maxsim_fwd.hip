@@ -20,6 +20,7 @@
 // Neither kernel writes the [Lq, Ld] similarity matrix anywhere: each
 // 32x32 MFMA tile is reduced in registers (tile_update) and discarded.
 #include <string>
+#include <type_traits>
 #include <cstdio>
 #include <cstdarg>
 
@@ -223,9 +224,14 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
 // ---------------------------------------------------------------------------
 // Workgroup = 8 waves.  Wave w holds NBW query blocks: queries
 // [q0 + w*qpw, q0 + (w+1)*qpw), each of nblk = ceil(Lq/32) blocks, with
-// qpw * nblk <= NBW.  Document tiles (32 rows x dim) are staged in LDS as
-// 16-byte pieces; piece index is XOR-swizzled with the row so the MFMA
-// operand reads (one row per lane) are bank-conflict free.
+// qpw * nblk <= NBW.  The workgroup walks the 32-row tiles of its chunk of
+// documents in order.  Each tile is fetched from global memory PF tiles
+// ahead into registers, written to one of two LDS buffers one tile ahead,
+// and read by all 8 waves as MFMA A-operands.  In LDS a tile is 32 rows of
+// 16-byte pieces; the piece index is XOR-swizzled with the row so the
+// operand reads (one row per lane) are bank-conflict free.  Requires
+// dim == KS*16 and 16-byte aligned rows (the host routes other shapes to
+// pair_kernel).
 constexpr int kTiledWaves = 8;
 constexpr int kTiledThreads = kTiledWaves * 64;
 
@@ -257,9 +263,16 @@ struct TileGeom {
   static constexpr int kBufPieces = kPieces;                // uint4 per buffer
 };
 
-template <typename T, int KS, int NBW, bool ARGMAX>
-__global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(
-    TiledArgs a, bool vec) {
+// Position in the (document, tile) walk of a workgroup.
+struct TileCursor {
+  int64_t b;      // document
+  int64_t row0;   // its first row
+  int ld;         // its length (0 when past the end)
+  int t;          // tile within the document
+};
+
+template <typename T, int KS, int NBW, bool ARGMAX, int PF>
+__global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledArgs a) {
   using S = typename T::storage;
   using G = TileGeom<T, KS>;
   extern __shared__ uint4 lds[];  // [2][32][P]
@@ -288,106 +301,105 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(
   Frag<T> qf[NBW][KS];
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
-    int64_t q = q_first + j / a.nblk;
-    q = min(q, a.nq - 1);
+    const int64_t q = min(q_first + j / a.nblk, a.nq - 1);
     const int part = j % a.nblk;
     const int tok = min(part * kTileCols + c, a.lq - 1);
     const S* row = Q + (q * a.lq + tok) * (int64_t)dim;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      qf[j][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+      qf[j][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, true);
   }
 
   const int64_t b_begin = (int64_t)dc * a.dpw;
   const int64_t b_end = min(b_begin + (int64_t)a.dpw, a.nb);
 
-  // Flattened walk over (doc, tile).  `cur_*` is the tile being computed,
-  // `nxt_*` the tile being fetched.
-  auto doc_len = [&](int64_t b, int64_t& s0) -> int {
+  auto doc_ok = [&](int64_t b, int64_t& s0, int& ld) {
     const int64_t s = a.doff[b], e = a.doff[b + 1];
     s0 = s;
-    const bool ok = (s >= 0) && (e > s) && (e <= a.total_d);
-    return ok ? (int)(e - s) : 0;
+    ld = (int)(e - s);
+    return (s >= 0) && (e > s) && (e <= a.total_d);
   };
-
-  uint4 stage[G::NP];
-  auto fetch = [&](int64_t row0, int ld, int t) {
-#pragma unroll
-    for (int i = 0; i < G::NP; ++i) {
-      const int piece = tid + i * kTiledThreads;
-      stage[i] = make_uint4(0, 0, 0, 0);
-      if (piece < G::kPieces) {
-        const int r = piece / G::P;
-        const int pc = piece - r * G::P;
-        const int row = min(t * kTileRows + r, ld - 1);
-        const S* src = D + (row0 + row) * (int64_t)dim;
-        const int k0 = pc * G::kPieceElems;
-        if (vec) {
-          stage[i] = *reinterpret_cast<const uint4*>(src + k0);
-        } else {
-          if constexpr (T::bytes == 2) {
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int k = k0 + 2 * e;
-              const uint32_t lo = (k < dim) ? (uint32_t)src[k] : 0u;
-              const uint32_t hi = (k + 1 < dim) ? (uint32_t)src[k + 1] : 0u;
-              w[e] = lo | (hi << 16);
-            }
-            stage[i] = make_uint4(w[0], w[1], w[2], w[3]);
-          } else {
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              w[e] = (k0 + e < dim) ? __float_as_uint(src[k0 + e]) : 0u;
-            stage[i] = make_uint4(w[0], w[1], w[2], w[3]);
-          }
-        }
-      }
-    }
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < G::NP; ++i) {
-      const int piece = tid + i * kTiledThreads;
-      if (piece < G::kPieces) {
-        const int r = piece / G::P;
-        const int pc = piece - r * G::P;
-        lds[buf * G::kBufPieces + r * G::P + (pc ^ (r & G::SWZ))] = stage[i];
-      }
-    }
-  };
-
-  // Find the first valid document of the chunk.
-  int64_t cur_b = b_begin, cur_row0 = 0;
-  int cur_ld = 0;
-  while (cur_b < b_end) {
-    cur_ld = doc_len(cur_b, cur_row0);
-    if (cur_ld > 0) break;
-    ++cur_b;
-  }
-  // Documents with invalid offsets get NaN scores / zero argmax.
-  auto write_invalid_doc = [&](int64_t b) {
+  // Documents with invalid offsets: NaN score, zero argmax, never read.
+  for (int64_t b = b_begin; b < b_end; ++b) {
+    int64_t s0;
+    int ld;
+    if (doc_ok(b, s0, ld)) continue;
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       const int64_t q = q_first + j / a.nblk;
       if (j >= a.qpw * a.nblk || q >= a.nq) continue;
-      const int part = j % a.nblk;
-      const int tok = part * kTileCols + c;
-      if (ARGMAX && h == 0 && tok < a.lq)
-        a.argmax[(q * a.nb + b) * a.lq + tok] = 0;
-      if (part == 0 && lane == 0) a.scores[q * a.nb + b] = __builtin_nanf("");
+      const int tok = (j % a.nblk) * kTileCols + c;
+      if (ARGMAX && h == 0 && tok < a.lq) a.argmax[(q * a.nb + b) * a.lq + tok] = 0;
+      if (j % a.nblk == 0 && lane == 0) a.scores[q * a.nb + b] = __builtin_nanf("");
+    }
+  }
+  // First valid document at or after b (cursor at its tile 0).
+  auto seek = [&](int64_t b) -> TileCursor {
+    TileCursor cur{b_end, 0, 0, 0};
+    for (; b < b_end; ++b) {
+      int64_t s0;
+      int ld;
+      if (doc_ok(b, s0, ld)) {
+        cur.b = b;
+        cur.row0 = s0;
+        cur.ld = ld;
+        break;
+      }
+    }
+    return cur;
+  };
+  auto advance = [&](TileCursor cur) -> TileCursor {
+    if (cur.b >= b_end) return cur;
+    if ((cur.t + 1) * kTileRows < cur.ld) {
+      ++cur.t;
+      return cur;
+    }
+    return seek(cur.b + 1);
+  };
+
+  // ---- tile staging: global -> registers (PF tiles ahead) -> LDS
+  uint4 st0[G::NP], st1[G::NP], st2[G::NP];
+  auto stage_ref = [&](auto k_const) -> uint4 (&)[G::NP] {
+    constexpr int K = decltype(k_const)::value % PF;
+    if constexpr (K == 0) return st0;
+    else if constexpr (K == 1) return st1;
+    else return st2;
+  };
+  auto fetch = [&](uint4 (&st)[G::NP], const TileCursor& cur) {
+#pragma unroll
+    for (int i = 0; i < G::NP; ++i) {
+      const int slot = tid + i * kTiledThreads;
+      if (slot < G::kPieces && cur.b < b_end) {
+        const int r = slot / G::P;
+        const int pc = (slot - r * G::P) ^ (r & G::SWZ);
+        const int row = min(cur.t * kTileRows + r, cur.ld - 1);
+        st[i] = *reinterpret_cast<const uint4*>(
+            D + (cur.row0 + row) * (int64_t)dim + pc * G::kPieceElems);
+      }
     }
   };
-  for (int64_t b = b_begin; b < cur_b; ++b) write_invalid_doc(b);
-  if (cur_b >= b_end) return;
+  auto commit = [&](const uint4 (&st)[G::NP], int buf) {
+#pragma unroll
+    for (int i = 0; i < G::NP; ++i) {
+      const int slot = tid + i * kTiledThreads;
+      if (slot < G::kPieces) lds[buf * G::kBufPieces + slot] = st[i];
+    }
+  };
 
-  fetch(cur_row0, cur_ld, 0);
-  commit(0);
+  TileCursor cc = seek(b_begin);
+  if (cc.b >= b_end) return;
+  TileCursor fc = cc;
+  fetch(st0, fc);
+  fc = advance(fc);
+  fetch(st1, fc);
+  fc = advance(fc);
+  if constexpr (PF == 3) {
+    fetch(st2, fc);
+    fc = advance(fc);
+  }
+  commit(st0, 0);
   __syncthreads();
 
-  int cur_t = 0;
-  int buf = 0;
   float m[NBW];
   int am[NBW];
 #pragma unroll
@@ -395,52 +407,61 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(
     m[j] = -__builtin_inff();
     am[j] = 0;
   }
-
-  while (true) {
-    // ---- decide and fetch the next tile (may belong to the next doc)
-    const int cur_ntiles = (cur_ld + kTileRows - 1) / kTileRows;
-    int64_t nxt_b = cur_b, nxt_row0 = cur_row0;
-    int nxt_ld = cur_ld, nxt_t = cur_t + 1;
-    int64_t skipped_from = -1, skipped_to = -1;
-    if (nxt_t >= cur_ntiles) {
-      nxt_t = 0;
-      nxt_b = cur_b + 1;
-      skipped_from = nxt_b;
-      nxt_ld = 0;
-      while (nxt_b < b_end) {
-        nxt_ld = doc_len(nxt_b, nxt_row0);
-        if (nxt_ld > 0) break;
-        ++nxt_b;
-      }
-      skipped_to = nxt_b;
+  // per-lane LDS word offsets of this lane's A fragments
+  int aoff[KS * (T::bytes == 2 ? 1 : 2)];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if constexpr (T::bytes == 2) {
+      aoff[s] = c * G::P + ((2 * s + h) ^ (c & G::SWZ));
+    } else {
+      aoff[2 * s] = c * G::P + ((4 * s + 2 * h) ^ (c & G::SWZ));
+      aoff[2 * s + 1] = c * G::P + ((4 * s + 2 * h + 1) ^ (c & G::SWZ));
     }
-    const bool have_next = nxt_b < b_end;
-    if (have_next) fetch(nxt_row0, nxt_ld, nxt_t);
+  }
 
-    // ---- compute on the current tile
+  int buf = 0;
+  // One step of the walk; U (the stage slot) is a compile-time constant so
+  // the register ring is never indexed dynamically.  Returns true when the
+  // last tile has been computed.
+  auto step = [&](auto u_const) __attribute__((always_inline)) -> bool {
+    constexpr int U = decltype(u_const)::value;
+    // stage[U] was committed last step; refill it with the tile PF ahead.
+    fetch(stage_ref(std::integral_constant<int, U>{}), fc);
+    fc = advance(fc);
+
+    const uint4* tile = lds + buf * G::kBufPieces;
     Frag<T> df[KS];
-    const uint4* tile = lds + buf * G::kBufPieces + c * G::P;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       if constexpr (T::bytes == 2) {
-        df[s].v = tile[(2 * s + h) ^ (c & G::SWZ)];
+        df[s].v = tile[aoff[s]];
       } else {
-        df[s].lo = tile[(4 * s + 2 * h) ^ (c & G::SWZ)];
-        df[s].hi = tile[(4 * s + 2 * h + 1) ^ (c & G::SWZ)];
+        df[s].lo = tile[aoff[2 * s]];
+        df[s].hi = tile[aoff[2 * s + 1]];
       }
     }
-    const int valid = cur_ld - cur_t * kTileRows;
+    f32x16 acc[NBW];
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-      f32x16 acc = {};
+      acc[j] = f32x16{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[j][s], acc);
-      if (valid < kTileRows) mask_rows(acc, h, valid);
-      tile_update<ARGMAX>(acc, m[j], am[j], cur_t * kTileRows + 4 * h);
+      for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[j][s], acc[j]);
+    }
+    const int valid = cc.ld - cc.t * kTileRows;
+    const int row_base = cc.t * kTileRows + 4 * h;
+    if (valid >= kTileRows) {
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        mask_rows(acc[j], h, valid);
+        tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
+      }
     }
 
-    // ---- end of document: finalize (query, doc) results
-    if (cur_t + 1 >= cur_ntiles) {
+    // ---- end of document: finalize the (query, document) results
+    if (valid <= kTileRows) {
       float part_sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < NBW; ++j) {
@@ -449,30 +470,32 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(
         merge_halves(m[j], am[j]);
         const int tok = part * kTileCols + c;
         const bool vtok = tok < a.lq;
-        const float s = half_sum(vtok ? m[j] : 0.0f);
-        part_sum = (part == 0) ? s : part_sum + s;
-        const bool q_ok = (j < a.qpw * a.nblk) && (q < a.nq);
-        if (q_ok) {
-          if (ARGMAX && h == 0 && vtok)
-            a.argmax[(q * a.nb + cur_b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == 0)
-            a.scores[q * a.nb + cur_b] = part_sum;
+        const float sm = half_sum(vtok ? m[j] : 0.0f);
+        part_sum = (part == 0) ? sm : part_sum + sm;
+        if ((j < a.qpw * a.nblk) && (q < a.nq)) {
+          if (ARGMAX && h == 0 && vtok) a.argmax[(q * a.nb + cc.b) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == 0) a.scores[q * a.nb + cc.b] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
       }
-      for (int64_t b = skipped_from; b >= 0 && b < skipped_to; ++b)
-        write_invalid_doc(b);
     }
 
-    if (!have_next) break;
-    commit(buf ^ 1);
+    cc = advance(cc);
+    if (cc.b >= b_end) return true;
+    // the next tile was fetched PF-1 steps ago into stage[(U + 1) % PF]
+    commit(stage_ref(std::integral_constant<int, U + 1>{}), buf ^ 1);
     __syncthreads();
     buf ^= 1;
-    cur_b = nxt_b;
-    cur_row0 = nxt_row0;
-    cur_ld = nxt_ld;
-    cur_t = nxt_t;
+    return false;
+  };
+  static_assert(PF == 2 || PF == 3, "prefetch depth");
+  while (true) {
+    if (step(std::integral_constant<int, 0>{})) break;
+    if (step(std::integral_constant<int, 1>{})) break;
+    if constexpr (PF == 3) {
+      if (step(std::integral_constant<int, 2>{})) break;
+    }
   }
 }
 
@@ -554,8 +577,10 @@ constexpr int tiled_nbw() {
   return (KS * (T::bytes == 2 ? 4 : 8) * 2 <= 64) ? 2 : 1;
 }
 
+constexpr int kTiledPrefetch = 3;  // tiles in flight from global memory
+
 template <typename T, int KS>
-static void launch_tiled_ks(TiledArgs a, bool vec, hipStream_t st) {
+static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   constexpr int NBW = tiled_nbw<T, KS>();
   using G = TileGeom<T, KS>;
   a.qpw = NBW / a.nblk;
@@ -573,11 +598,11 @@ static void launch_tiled_ks(TiledArgs a, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)(per_xcd * 8));
   const size_t lds = 2 * G::kBufPieces * sizeof(uint4);
   if (a.argmax)
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
-                       dim3(kTiledThreads), lds, st, a, vec);
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true, kTiledPrefetch>), grid,
+                       dim3(kTiledThreads), lds, st, a);
   else
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false>), grid,
-                       dim3(kTiledThreads), lds, st, a, vec);
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false, kTiledPrefetch>), grid,
+                       dim3(kTiledThreads), lds, st, a);
 }
 
 template <typename T>
@@ -595,12 +620,12 @@ static bool tiled_supported(int dim, int lq) {
 }
 
 template <typename T>
-static void launch_tiled(const TiledArgs& a, bool vec, hipStream_t st) {
+static void launch_tiled(const TiledArgs& a, hipStream_t st) {
   switch (ks_for_dim(a.dim)) {
-    case 2: launch_tiled_ks<T, 2>(a, vec, st); break;
-    case 4: launch_tiled_ks<T, 4>(a, vec, st); break;
-    case 8: launch_tiled_ks<T, 8>(a, vec, st); break;
-    default: launch_tiled_ks<T, 16>(a, vec, st); break;
+    case 2: launch_tiled_ks<T, 2>(a, st); break;
+    case 4: launch_tiled_ks<T, 4>(a, st); break;
+    case 8: launch_tiled_ks<T, 8>(a, st); break;
+    default: launch_tiled_ks<T, 16>(a, st); break;
   }
 }
 
@@ -616,7 +641,9 @@ static int run_contrastive(maxsim_dtype dtype, const void* q, int64_t nq,
     case MAXSIM_FLOAT16: tiled = tiled_supported<F16>((int)dim, (int)lq); break;
     default: tiled = tiled_supported<F32>((int)dim, (int)lq); break;
   }
-  if (tiled) {
+  // The tiled kernel stages whole 16-byte pieces: it needs dim == KS*16 and
+  // aligned rows; other shapes take the pair kernel.
+  if (tiled && vec) {
     TiledArgs a{};
     a.q = q;
     a.d = d;
@@ -630,9 +657,9 @@ static int run_contrastive(maxsim_dtype dtype, const void* q, int64_t nq,
     a.scores = scores;
     a.argmax = argmax;
     switch (dtype) {
-      case MAXSIM_BFLOAT16: launch_tiled<BF16>(a, vec, st); break;
-      case MAXSIM_FLOAT16: launch_tiled<F16>(a, vec, st); break;
-      default: launch_tiled<F32>(a, vec, st); break;
+      case MAXSIM_BFLOAT16: launch_tiled<BF16>(a, st); break;
+      case MAXSIM_FLOAT16: launch_tiled<F16>(a, st); break;
+      default: launch_tiled<F32>(a, st); break;
     }
     return check_launch("contrastive_tiled_kernel");
   }
