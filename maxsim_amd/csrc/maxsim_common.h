@@ -123,23 +123,20 @@ __device__ __forceinline__ constexpr int acc_row(int r, int h) {
   return 8 * (r >> 2) + 4 * h + (r & 3);
 }
 
-// Rows at or beyond `valid` (only in a document's last, partial tile) must
-// never win: they were loaded from a clamped row and are forced to -inf.
-__device__ __forceinline__ void mask_rows(f32x16& acc, int h, int valid) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r)
-    if (acc_row(r, h) >= valid) acc[r] = -__builtin_inff();
-}
-
 // Running max / argmax update for one tile.  Semantics (shared with the
 // reference kernels, maxsim.cu:412-443): ascending document order, strict
 // `>` so the first index wins ties, NaN never wins (fmaxf ignores NaN and
 // `>`/`==` are false for NaN).  `row_base` is tile_row0 + 4*h.
 //
-// Cost: a max3 tree (8 VALU) per tile; only when the tile beats the running
-// max, the first register equal to the tile max is located.  The sixteen
-// equality tests are independent (no compare -> select hazard chain) and the
-// selected constant is the register's row offset 8*(r>>2) + (r&3).
+// Rows past the end of a document are never masked: the kernels load them
+// as copies of the document's last row, whose similarities are bitwise equal
+// and come later, so under the strict `>` they can neither raise the max nor
+// take the argmax.
+//
+// The update is branch-free (a max3 tree, then the first register equal to
+// the tile max -- sixteen independent compares feeding a select chain --,
+// then a conditional commit), so it forms one scheduling region with the
+// MFMAs of the next tile and its VALU work can fill the MFMA shadow.
 template <bool ARGMAX>
 __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
                                             int& am, int row_base) {
@@ -151,17 +148,16 @@ __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
   const float t5 = fmaxf(fmaxf(t0, t1), t2);
   const float t6 = fmaxf(fmaxf(t3, t4), acc[15]);
   const float tmax = fmaxf(t5, t6);
-  if (tmax > m) {
-    m = tmax;
-    if constexpr (ARGMAX) {
-      bool eq[16];
+  const bool upd = tmax > m;
+  m = upd ? tmax : m;
+  if constexpr (ARGMAX) {
+    bool eq[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) eq[r] = acc[r] == tmax;
-      int off = 8 * (15 >> 2) + (15 & 3);
+    for (int r = 0; r < 16; ++r) eq[r] = acc[r] == tmax;
+    int off = 8 * (15 >> 2) + (15 & 3);
 #pragma unroll
-      for (int r = 14; r >= 0; --r) off = eq[r] ? (8 * (r >> 2) + (r & 3)) : off;
-      am = row_base + off;
-    }
+    for (int r = 14; r >= 0; --r) off = eq[r] ? (8 * (r >> 2) + (r & 3)) : off;
+    am = upd ? row_base + off : am;
   }
 }
 

@@ -184,15 +184,18 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
           for (int s = 0; s < KS; ++s)
             nf[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
         }
-        const int valid = pr.ld - t * kTileRows;
+        // rows past the document end were loaded as copies of its last row
+        // and cannot win (see tile_update), so no masking is needed
+        f32x16 acc[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          f32x16 acc = {};
+          acc[qb] = f32x16{};
 #pragma unroll
-          for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc);
-          if (valid < kTileRows) mask_rows(acc, h, valid);
-          tile_update<ARGMAX>(acc, m[qb], am[qb], t * kTileRows + 4 * h);
+          for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
         }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
         if (t + 1 < ntiles) {
 #pragma unroll
           for (int s = 0; s < KS; ++s) df[s] = nf[s];
@@ -225,9 +228,11 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
 // Workgroup = 8 waves.  Wave w holds NBW query blocks: queries
 // [q0 + w*qpw, q0 + (w+1)*qpw), each of nblk = ceil(Lq/32) blocks, with
 // qpw * nblk <= NBW.  The workgroup walks the 32-row tiles of its chunk of
-// documents in order.  Each tile is fetched from global memory PF tiles
-// ahead into registers, written to one of two LDS buffers one tile ahead,
-// and read by all 8 waves as MFMA A-operands.  In LDS a tile is 32 rows of
+// documents in order.  Each tile is fetched from global memory into
+// registers four steps ahead, written to one of two LDS buffers two steps
+// ahead, and read by all 8 waves as MFMA A-operands one step ahead, so the
+// max/argmax epilogue of one tile runs while the MFMAs of the next are in
+// flight.  In LDS a tile is 32 rows of
 // 16-byte pieces; the piece index is XOR-swizzled with the row so the
 // operand reads (one row per lane) are bank-conflict free.  Requires
 // dim == KS*16 and 16-byte aligned rows (the host routes other shapes to
@@ -271,7 +276,7 @@ struct TileCursor {
   int t;          // tile within the document
 };
 
-template <typename T, int KS, int NBW, bool ARGMAX, int PF>
+template <typename T, int KS, int NBW, bool ARGMAX>
 __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledArgs a) {
   using S = typename T::storage;
   using G = TileGeom<T, KS>;
@@ -357,14 +362,22 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     return seek(cur.b + 1);
   };
 
-  // ---- tile staging: global -> registers (PF tiles ahead) -> LDS
-  uint4 st0[G::NP], st1[G::NP], st2[G::NP];
-  auto stage_ref = [&](auto k_const) -> uint4 (&)[G::NP] {
-    constexpr int K = decltype(k_const)::value % PF;
-    if constexpr (K == 0) return st0;
-    else if constexpr (K == 1) return st1;
-    else return st2;
-  };
+  // ---- software pipeline
+  // Step k: (1) read the A fragments of tile k+1 from LDS and issue its
+  // MFMAs into one accumulator set, (2) run the max/argmax epilogue of tile k
+  // from the other set -- the VALU work overlaps the MFMAs in flight --,
+  // (3) write tile k+2 from registers into the LDS buffer tile k used, and
+  // refill those registers with tile k+4 from global memory, (4) barrier.
+  // LDS holds two tiles; each global fetch has two steps to land.
+  int ntiles = 0;
+  for (int64_t b = b_begin; b < b_end; ++b) {
+    int64_t s0;
+    int ld;
+    if (doc_ok(b, s0, ld)) ntiles += (ld + kTileRows - 1) / kTileRows;
+  }
+  if (ntiles == 0) return;
+
+  uint4 st0[G::NP], st1[G::NP];
   auto fetch = [&](uint4 (&st)[G::NP], const TileCursor& cur) {
 #pragma unroll
     for (int i = 0; i < G::NP; ++i) {
@@ -385,28 +398,6 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       if (slot < G::kPieces) lds[buf * G::kBufPieces + slot] = st[i];
     }
   };
-
-  TileCursor cc = seek(b_begin);
-  if (cc.b >= b_end) return;
-  TileCursor fc = cc;
-  fetch(st0, fc);
-  fc = advance(fc);
-  fetch(st1, fc);
-  fc = advance(fc);
-  if constexpr (PF == 3) {
-    fetch(st2, fc);
-    fc = advance(fc);
-  }
-  commit(st0, 0);
-  __syncthreads();
-
-  float m[NBW];
-  int am[NBW];
-#pragma unroll
-  for (int j = 0; j < NBW; ++j) {
-    m[j] = -__builtin_inff();
-    am[j] = 0;
-  }
   // per-lane LDS word offsets of this lane's A fragments
   int aoff[KS * (T::bytes == 2 ? 1 : 2)];
 #pragma unroll
@@ -418,17 +409,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       aoff[2 * s + 1] = c * G::P + ((4 * s + 2 * h + 1) ^ (c & G::SWZ));
     }
   }
-
-  int buf = 0;
-  // One step of the walk; U (the stage slot) is a compile-time constant so
-  // the register ring is never indexed dynamically.  Returns true when the
-  // last tile has been computed.
-  auto step = [&](auto u_const) __attribute__((always_inline)) -> bool {
-    constexpr int U = decltype(u_const)::value;
-    // stage[U] was committed last step; refill it with the tile PF ahead.
-    fetch(stage_ref(std::integral_constant<int, U>{}), fc);
-    fc = advance(fc);
-
+  auto mfma_tile = [&](int buf, f32x16 (&acc)[NBW]) {
     const uint4* tile = lds + buf * G::kBufPieces;
     Frag<T> df[KS];
 #pragma unroll
@@ -440,28 +421,36 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         df[s].hi = tile[aoff[2 * s + 1]];
       }
     }
-    f32x16 acc[NBW];
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       acc[j] = f32x16{};
 #pragma unroll
       for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[j][s], acc[j]);
     }
-    const int valid = cc.ld - cc.t * kTileRows;
-    const int row_base = cc.t * kTileRows + 4 * h;
-    if (valid >= kTileRows) {
-#pragma unroll
-      for (int j = 0; j < NBW; ++j) tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
-    } else {
-#pragma unroll
-      for (int j = 0; j < NBW; ++j) {
-        mask_rows(acc[j], h, valid);
-        tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
-      }
-    }
+  };
 
-    // ---- end of document: finalize the (query, document) results
-    if (valid <= kTileRows) {
+  float m[NBW];
+  int am[NBW];
+#pragma unroll
+  for (int j = 0; j < NBW; ++j) {
+    m[j] = -__builtin_inff();
+    am[j] = 0;
+  }
+  auto epilogue = [&](f32x16 (&acc)[NBW], const TileCursor& cur) {
+    const int valid = cur.ld - cur.t * kTileRows;
+    const int row_base = cur.t * kTileRows + 4 * h;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
+    // Interleave the epilogue's VALU work with the next tile's MFMAs so one
+    // wave keeps both pipes busy: LDS operand reads first, then alternate.
+#pragma unroll
+    for (int s = 0; s < KS; ++s) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < NBW * KS * (T::bytes == 2 ? 1 : 8); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, ARGMAX ? 5 : 2, 0);
+    }
+    if (valid <= kTileRows) {  // last tile of the document
       float part_sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < NBW; ++j) {
@@ -473,29 +462,60 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
-          if (ARGMAX && h == 0 && vtok) a.argmax[(q * a.nb + cc.b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == 0) a.scores[q * a.nb + cc.b] = part_sum;
+          if (ARGMAX && h == 0 && vtok) a.argmax[(q * a.nb + cur.b) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == 0) a.scores[q * a.nb + cur.b] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
       }
     }
+  };
 
-    cc = advance(cc);
-    if (cc.b >= b_end) return true;
-    // the next tile was fetched PF-1 steps ago into stage[(U + 1) % PF]
-    commit(stage_ref(std::integral_constant<int, U + 1>{}), buf ^ 1);
+  // ---- prologue: tiles 0 and 1 into LDS, tiles 2 and 3 in flight
+  TileCursor cc = seek(b_begin);      // tile k (epilogue)
+  TileCursor fc = cc;                 // next tile to fetch
+  fetch(st0, fc);
+  fc = advance(fc);
+  fetch(st1, fc);
+  fc = advance(fc);
+  commit(st0, 0);
+  __syncthreads();
+  f32x16 acc0[NBW], acc1[NBW];
+  mfma_tile(0, acc0);
+  commit(st1, 1);
+  fetch(st0, fc);   // tile 2
+  fc = advance(fc);
+  fetch(st1, fc);   // tile 3
+  fc = advance(fc);
+  __syncthreads();
+
+  // One pipeline step; U = k % 2 selects the accumulator set and the
+  // staging registers statically (no dynamic register indexing).
+  int k = 0;
+  auto step = [&](auto u_const) __attribute__((always_inline)) -> bool {
+    constexpr int U = decltype(u_const)::value;
+    f32x16 (&acc_cur)[NBW] = (U == 0) ? acc0 : acc1;
+    f32x16 (&acc_nxt)[NBW] = (U == 0) ? acc1 : acc0;
+    uint4 (&stg)[G::NP] = (U == 0) ? st0 : st1;
+    // Tile k+1 lives in buffer (k+1)&1.  The MFMAs are issued even after the
+    // last tile (reading a stale buffer, results unused) so the accumulator
+    // sets never merge control-flow paths and stay in fixed registers.
+    mfma_tile(U ^ 1, acc_nxt);
+    epilogue(acc_cur, cc);
+    if (k + 1 >= ntiles) return true;
+    if (k + 2 < ntiles) {
+      commit(stg, U);                            // tile k+2 -> buffer k&1
+      fetch(stg, fc);                            // tile k+4
+      fc = advance(fc);
+    }
     __syncthreads();
-    buf ^= 1;
+    cc = advance(cc);
+    ++k;
     return false;
   };
-  static_assert(PF == 2 || PF == 3, "prefetch depth");
   while (true) {
     if (step(std::integral_constant<int, 0>{})) break;
     if (step(std::integral_constant<int, 1>{})) break;
-    if constexpr (PF == 3) {
-      if (step(std::integral_constant<int, 2>{})) break;
-    }
   }
 }
 
@@ -577,8 +597,6 @@ constexpr int tiled_nbw() {
   return (KS * (T::bytes == 2 ? 4 : 8) * 2 <= 64) ? 2 : 1;
 }
 
-constexpr int kTiledPrefetch = 3;  // tiles in flight from global memory
-
 template <typename T, int KS>
 static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   constexpr int NBW = tiled_nbw<T, KS>();
@@ -598,10 +616,10 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   const dim3 grid((unsigned)(per_xcd * 8));
   const size_t lds = 2 * G::kBufPieces * sizeof(uint4);
   if (a.argmax)
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true, kTiledPrefetch>), grid,
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
                        dim3(kTiledThreads), lds, st, a);
   else
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false, kTiledPrefetch>), grid,
+    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false>), grid,
                        dim3(kTiledThreads), lds, st, a);
 }
 
