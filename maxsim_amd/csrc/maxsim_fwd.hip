@@ -239,6 +239,8 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
 // pair_kernel).
 constexpr int kTiledWaves = 8;
 constexpr int kTiledThreads = kTiledWaves * 64;
+constexpr int kTileBuffers = 4;        // LDS tile ring
+constexpr int kMaxDocsPerGroup = 256;  // LDS offset table per workgroup
 
 struct TiledArgs {
   const void* q;
@@ -257,6 +259,25 @@ struct TiledArgs {
   float* scores;
   int32_t* argmax;
 };
+
+// One 16-byte piece per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane i of the wave writes bytes
+// [16*i, 16*i + 16) after `dst`, which must be wave-uniform.  Written as
+// inline asm so the compiler does not pair every later LDS read with a
+// conservative wait for all loads in flight; the kernel orders these loads
+// itself (s_waitcnt vmcnt + s_barrier).  Loads complete in issue order, so
+// the compiler's own vmcnt waits stay correct (they can only get stricter).
+__device__ __forceinline__ void lds_dma16(const void* src, uint4* dst) {
+  // generic -> LDS address space gives the 32-bit LDS byte address
+  const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) void*)dst);
+  __asm__ __volatile__(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+      : "memory", "m0");
+}
 
 template <typename T, int KS>
 struct TileGeom {
@@ -280,7 +301,7 @@ template <typename T, int KS, int NBW, bool ARGMAX>
 __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledArgs a) {
   using S = typename T::storage;
   using G = TileGeom<T, KS>;
-  extern __shared__ uint4 lds[];  // [2][32][P]
+  extern __shared__ uint4 lds[];  // [4][32][P]
 
   // XCD-aware mapping: consecutive hardware workgroup ids go round-robin over
   // the 8 XCDs; give each XCD a contiguous range of logical ids, ordered
@@ -317,9 +338,18 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
 
   const int64_t b_begin = (int64_t)dc * a.dpw;
   const int64_t b_end = min(b_begin + (int64_t)a.dpw, a.nb);
+  float* __restrict__ scores = a.scores;
+  int32_t* __restrict__ argmax_out = a.argmax;
+  // The chunk's document offsets are copied to LDS once, so the tile walk
+  // never issues global loads of its own: the only vector-memory loads in
+  // flight are the tile loads, whose completion is tracked by count.
+  int* doff_lds = reinterpret_cast<int*>(lds + kTileBuffers * G::kBufPieces);
+  for (int64_t i = tid; i <= b_end - b_begin; i += kTiledThreads)
+    doff_lds[i] = a.doff[b_begin + i];
+  __syncthreads();
 
   auto doc_ok = [&](int64_t b, int64_t& s0, int& ld) {
-    const int64_t s = a.doff[b], e = a.doff[b + 1];
+    const int64_t s = doff_lds[b - b_begin], e = doff_lds[b - b_begin + 1];
     s0 = s;
     ld = (int)(e - s);
     return (s >= 0) && (e > s) && (e <= a.total_d);
@@ -334,8 +364,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       const int64_t q = q_first + j / a.nblk;
       if (j >= a.qpw * a.nblk || q >= a.nq) continue;
       const int tok = (j % a.nblk) * kTileCols + c;
-      if (ARGMAX && h == 0 && tok < a.lq) a.argmax[(q * a.nb + b) * a.lq + tok] = 0;
-      if (j % a.nblk == 0 && lane == 0) a.scores[q * a.nb + b] = __builtin_nanf("");
+      if (ARGMAX && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
+      if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
     }
   }
   // First valid document at or after b (cursor at its tile 0).
@@ -363,12 +393,21 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   };
 
   // ---- software pipeline
-  // Step k: (1) read the A fragments of tile k+1 from LDS and issue its
-  // MFMAs into one accumulator set, (2) run the max/argmax epilogue of tile k
-  // from the other set -- the VALU work overlaps the MFMAs in flight --,
-  // (3) write tile k+2 from registers into the LDS buffer tile k used, and
-  // refill those registers with tile k+4 from global memory, (4) barrier.
-  // LDS holds two tiles; each global fetch has two steps to land.
+  // LDS holds kNB = 4 tile buffers filled by direct global->LDS loads
+  // (global_load_lds_dwordx4: each lane moves one 16-byte piece, a wave
+  // instruction fills 1 KB of a buffer; the swizzle is applied by choosing
+  // the source address of each slot).  Step k:
+  //   (1) wait until this wave's loads of tile k+1 have landed, barrier --
+  //       now every wave's loads of tile k+1 are in LDS and every wave has
+  //       finished reading tile k;
+  //   (2) issue the loads of tile k+4 into tile k's buffer;
+  //   (3) read tile k+1's A fragments and issue its MFMAs into one
+  //       accumulator set;
+  //   (4) run the max/argmax epilogue of tile k from the other set -- its
+  //       VALU work is interleaved with the MFMAs in flight.
+  // Loads therefore have three steps to land and no registers are spent on
+  // staging.  Vector-memory loads complete in issue order, so "at most N
+  // loads outstanding" (s_waitcnt vmcnt(N)) identifies completed tiles.
   int ntiles = 0;
   for (int64_t b = b_begin; b < b_end; ++b) {
     int64_t s0;
@@ -377,28 +416,50 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   }
   if (ntiles == 0) return;
 
-  uint4 st0[G::NP], st1[G::NP];
-  auto fetch = [&](uint4 (&st)[G::NP], const TileCursor& cur) {
+  constexpr int kNB = kTileBuffers;
+  constexpr int kDmaPerTile = G::kPieces / 64;  // wave instructions per tile
+  static_assert(G::kPieces % 64 == 0, "tile must be whole wave loads");
+  // wave w issues instructions j = w, w + 8, ...; d_w of them per tile
+  const int d_w = (kDmaPerTile - wave + kTiledWaves - 1) / kTiledWaves;
+  auto dma_tile = [&](int buf, const TileCursor& cur) __attribute__((always_inline)) {
+    if (cur.b >= b_end) return;
 #pragma unroll
-    for (int i = 0; i < G::NP; ++i) {
-      const int slot = tid + i * kTiledThreads;
-      if (slot < G::kPieces && cur.b < b_end) {
+    for (int i = 0; i < (kDmaPerTile + kTiledWaves - 1) / kTiledWaves; ++i) {
+      const int j = wave + i * kTiledWaves;
+      if (j < kDmaPerTile) {
+        const int slot = j * 64 + lane;
         const int r = slot / G::P;
         const int pc = (slot - r * G::P) ^ (r & G::SWZ);
         const int row = min(cur.t * kTileRows + r, cur.ld - 1);
-        st[i] = *reinterpret_cast<const uint4*>(
-            D + (cur.row0 + row) * (int64_t)dim + pc * G::kPieceElems);
+        const S* src = D + (cur.row0 + row) * (int64_t)dim + pc * G::kPieceElems;
+        lds_dma16(src, lds + buf * G::kBufPieces + j * 64);
       }
     }
   };
-  auto commit = [&](const uint4 (&st)[G::NP], int buf) {
-#pragma unroll
-    for (int i = 0; i < G::NP; ++i) {
-      const int slot = tid + i * kTiledThreads;
-      if (slot < G::kPieces) lds[buf * G::kBufPieces + slot] = st[i];
+  // s_waitcnt vmcnt(n) for the runtime n in {0, 1, 2, 3, 4, 6}; other waits
+  // fall back to vmcnt(0).  Encoding (gfx9): vmcnt[3:0] | expcnt[6:4] = 7 |
+  // lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14.
+  auto wait_vm = [&](int n) __attribute__((always_inline)) {
+    switch (n) {
+      case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
     }
   };
-  // per-lane LDS word offsets of this lane's A fragments
+
+  // s_barrier without a memory fence (a fence would wait for every load in
+  // flight); the empty asm statements keep the compiler from moving memory
+  // accesses across it.
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+  };
+
+  // per-lane LDS element offsets of this lane's A fragments in buffer 0
   int aoff[KS * (T::bytes == 2 ? 1 : 2)];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -409,8 +470,9 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       aoff[2 * s + 1] = c * G::P + ((4 * s + 2 * h + 1) ^ (c & G::SWZ));
     }
   }
-  auto mfma_tile = [&](int buf, f32x16 (&acc)[NBW]) {
-    const uint4* tile = lds + buf * G::kBufPieces;
+  auto mfma_tile = [&](auto buf_const, f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_const)::value;
+    const uint4* tile = lds + BUF * G::kBufPieces;
     Frag<T> df[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -436,7 +498,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     m[j] = -__builtin_inff();
     am[j] = 0;
   }
-  auto epilogue = [&](f32x16 (&acc)[NBW], const TileCursor& cur) {
+  auto epilogue = [&](f32x16 (&acc)[NBW], const TileCursor& cur) __attribute__((always_inline)) {
     const int valid = cur.ld - cur.t * kTileRows;
     const int row_base = cur.t * kTileRows + 4 * h;
 #pragma unroll
@@ -445,6 +507,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     // wave keeps both pipes busy: LDS operand reads first, then alternate.
 #pragma unroll
     for (int s = 0; s < KS; ++s) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
 #pragma unroll
     for (int i = 0; i < NBW * KS * (T::bytes == 2 ? 1 : 8); ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -462,8 +525,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
-          if (ARGMAX && h == 0 && vtok) a.argmax[(q * a.nb + cur.b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == 0) a.scores[q * a.nb + cur.b] = part_sum;
+          if (ARGMAX && h == 0 && vtok) argmax_out[(q * a.nb + cur.b) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == 0) scores[q * a.nb + cur.b] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
@@ -471,44 +534,33 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     }
   };
 
-  // ---- prologue: tiles 0 and 1 into LDS, tiles 2 and 3 in flight
+  // ---- prologue: loads of tiles 0..3 in flight, tile 0's MFMAs issued
   TileCursor cc = seek(b_begin);      // tile k (epilogue)
-  TileCursor fc = cc;                 // next tile to fetch
-  fetch(st0, fc);
-  fc = advance(fc);
-  fetch(st1, fc);
-  fc = advance(fc);
-  commit(st0, 0);
-  __syncthreads();
+  TileCursor fc = cc;                 // next tile to load
+#pragma unroll
+  for (int i = 0; i < kNB; ++i) {
+    dma_tile(i, fc);
+    fc = advance(fc);
+  }
+  wait_vm(ntiles >= kNB ? (kNB - 1) * d_w : 0);
+  barrier();
   f32x16 acc0[NBW], acc1[NBW];
-  mfma_tile(0, acc0);
-  commit(st1, 1);
-  fetch(st0, fc);   // tile 2
-  fc = advance(fc);
-  fetch(st1, fc);   // tile 3
-  fc = advance(fc);
-  __syncthreads();
+  mfma_tile(std::integral_constant<int, 0>{}, acc0);
 
-  // One pipeline step; U = k % 2 selects the accumulator set and the
-  // staging registers statically (no dynamic register indexing).
   int k = 0;
   auto step = [&](auto u_const) __attribute__((always_inline)) -> bool {
-    constexpr int U = decltype(u_const)::value;
-    f32x16 (&acc_cur)[NBW] = (U == 0) ? acc0 : acc1;
-    f32x16 (&acc_nxt)[NBW] = (U == 0) ? acc1 : acc0;
-    uint4 (&stg)[G::NP] = (U == 0) ? st0 : st1;
-    // Tile k+1 lives in buffer (k+1)&1.  The MFMAs are issued even after the
-    // last tile (reading a stale buffer, results unused) so the accumulator
-    // sets never merge control-flow paths and stay in fixed registers.
-    mfma_tile(U ^ 1, acc_nxt);
+    constexpr int U = decltype(u_const)::value;  // k % 4
+    f32x16 (&acc_cur)[NBW] = (U % 2 == 0) ? acc0 : acc1;
+    f32x16 (&acc_nxt)[NBW] = (U % 2 == 0) ? acc1 : acc0;
+    // tile k+1 must be resident (it is read below even past the last tile:
+    // the results are then unused, but every wave must keep the barriers)
+    wait_vm(k + kNB - 1 < ntiles ? (kNB - 2) * d_w : 0);
+    barrier();
+    dma_tile(U, fc);                                  // tile k+4 -> buffer k % 4
+    fc = advance(fc);
+    mfma_tile(std::integral_constant<int, (U + 1) % kNB>{}, acc_nxt);
     epilogue(acc_cur, cc);
     if (k + 1 >= ntiles) return true;
-    if (k + 2 < ntiles) {
-      commit(stg, U);                            // tile k+2 -> buffer k&1
-      fetch(stg, fc);                            // tile k+4
-      fc = advance(fc);
-    }
-    __syncthreads();
     cc = advance(cc);
     ++k;
     return false;
@@ -516,7 +568,11 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   while (true) {
     if (step(std::integral_constant<int, 0>{})) break;
     if (step(std::integral_constant<int, 1>{})) break;
+    if (step(std::integral_constant<int, 2>{})) break;
+    if (step(std::integral_constant<int, 3>{})) break;
   }
+  // drain: no load may still be writing LDS when the workgroup exits
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // ---------------------------------------------------------------------------
@@ -599,6 +655,9 @@ constexpr int tiled_nbw() {
 
 template <typename T, int KS>
 static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
+  if constexpr (4 * 32 * KS * 16 * T::bytes + 4 * (kMaxDocsPerGroup + 1) > 64 * 1024) {
+    return;  // excluded by tiled_supported(): four buffers would exceed 64 KB
+  } else {
   constexpr int NBW = tiled_nbw<T, KS>();
   using G = TileGeom<T, KS>;
   a.qpw = NBW / a.nblk;
@@ -608,24 +667,31 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   // documents together so every workgroup streams a long tile sequence.
   int64_t n_dc = (2048 + a.n_qg - 1) / a.n_qg;
   if (n_dc > a.nb) n_dc = a.nb;
+  if (n_dc < (a.nb + kMaxDocsPerGroup - 1) / kMaxDocsPerGroup)
+    n_dc = (a.nb + kMaxDocsPerGroup - 1) / kMaxDocsPerGroup;
   if (n_dc < 1) n_dc = 1;
   a.dpw = (int)((a.nb + n_dc - 1) / n_dc);
   a.n_dc = (int)((a.nb + a.dpw - 1) / a.dpw);
   const int64_t total = (int64_t)a.n_qg * a.n_dc;
   const int64_t per_xcd = (total + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8));
-  const size_t lds = 2 * G::kBufPieces * sizeof(uint4);
+  const size_t lds = kTileBuffers * G::kBufPieces * sizeof(uint4) +
+                     (kMaxDocsPerGroup + 1) * sizeof(int);
   if (a.argmax)
     hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
                        dim3(kTiledThreads), lds, st, a);
   else
     hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false>), grid,
                        dim3(kTiledThreads), lds, st, a);
+  }
 }
 
 template <typename T>
 static bool tiled_supported(int dim, int lq) {
   const int ks = ks_for_dim(dim);
+  // four LDS tile buffers of 32 rows x ks*16 elements (plus the offset
+  // table) must fit in 64 KB
+  if (4 * 32 * ks * 16 * T::bytes + 4 * (kMaxDocsPerGroup + 1) > 64 * 1024) return false;
   int nbw = 1;
   switch (ks) {
     case 2: nbw = tiled_nbw<T, 2>(); break;
