@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       const int64_t q = q_first + j / a.nblk;
       if (j >= a.qpw * a.nblk || q >= a.nq) continue;
       const int tok = (j % a.nblk) * kTileCols + c;
-      if (ARGMAX && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
+      if (ARGMAX && argmax_out && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
       if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
     }
   }
@@ -397,16 +397,16 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // (global_load_lds_dwordx4: each lane moves one 16-byte piece, a wave
   // instruction fills 1 KB of a buffer; the swizzle is applied by choosing
   // the source address of each slot).  Step k:
-  //   (1) wait until this wave's loads of tile k+1 have landed, barrier --
-  //       now every wave's loads of tile k+1 are in LDS and every wave has
-  //       finished reading tile k;
+  //   (1) wait until this wave's loads of tile k+2 have landed, barrier --
+  //       now every wave's loads of tile k+2 are in LDS and every wave has
+  //       finished reading tile k's buffer (read two steps earlier);
   //   (2) issue the loads of tile k+4 into tile k's buffer;
-  //   (3) read tile k+1's A fragments and issue its MFMAs into one
-  //       accumulator set;
+  //   (3) issue tile k+1's MFMAs from A fragments already in registers
+  //       into one accumulator set, and read tile k+2's fragments;
   //   (4) run the max/argmax epilogue of tile k from the other set -- its
-  //       VALU work is interleaved with the MFMAs in flight.
-  // Loads therefore have three steps to land and no registers are spent on
-  // staging.  Vector-memory loads complete in issue order, so "at most N
+  //       VALU work and the LDS reads are interleaved with the MFMAs.
+  // Loads have two steps to land, operand reads a whole step, and no
+  // registers are spent on global->LDS staging.  Vector-memory loads complete in issue order, so "at most N
   // loads outstanding" (s_waitcnt vmcnt(N)) identifies completed tiles.
   int ntiles = 0;
   for (int64_t b = b_begin; b < b_end; ++b) {
@@ -470,10 +470,9 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       aoff[2 * s + 1] = c * G::P + ((4 * s + 2 * h + 1) ^ (c & G::SWZ));
     }
   }
-  auto mfma_tile = [&](auto buf_const, f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
+  auto read_frags = [&](auto buf_const, Frag<T> (&df)[KS]) __attribute__((always_inline)) {
     constexpr int BUF = decltype(buf_const)::value;
     const uint4* tile = lds + BUF * G::kBufPieces;
-    Frag<T> df[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       if constexpr (T::bytes == 2) {
@@ -483,6 +482,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         df[s].hi = tile[aoff[2 * s + 1]];
       }
     }
+  };
+  auto mfma_tile = [&](const Frag<T> (&df)[KS], f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       acc[j] = f32x16{};
@@ -503,14 +504,13 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     const int row_base = cur.t * kTileRows + 4 * h;
 #pragma unroll
     for (int j = 0; j < NBW; ++j) tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
-    // Interleave the epilogue's VALU work with the next tile's MFMAs so one
-    // wave keeps both pipes busy: LDS operand reads first, then alternate.
-#pragma unroll
-    for (int s = 0; s < KS; ++s) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    // Interleave the epilogue's VALU work and the operand reads for the tile
+    // after next with the next tile's MFMAs, so one wave keeps the MFMA,
+    // VALU and LDS pipes busy at once.
 #pragma unroll
     for (int i = 0; i < NBW * KS * (T::bytes == 2 ? 1 : 8); ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < KS * (T::bytes == 2 ? 1 : 2)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, ARGMAX ? 5 : 2, 0);
     }
     if (valid <= kTileRows) {  // last tile of the document
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
-          if (ARGMAX && h == 0 && vtok) argmax_out[(q * a.nb + cur.b) * a.lq + tok] = am[j];
+          if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + cur.b) * a.lq + tok] = am[j];
           if (part == a.nblk - 1 && lane == 0) scores[q * a.nb + cur.b] = part_sum;
         }
         m[j] = -__builtin_inff();
@@ -534,7 +534,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     }
   };
 
-  // ---- prologue: loads of tiles 0..3 in flight, tile 0's MFMAs issued
+  // ---- prologue: loads of tiles 0..3 issued; fragments of tiles 0 and 1
+  // in registers; tile 0's MFMAs issued
   TileCursor cc = seek(b_begin);      // tile k (epilogue)
   TileCursor fc = cc;                 // next tile to load
 #pragma unroll
@@ -542,23 +543,33 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     dma_tile(i, fc);
     fc = advance(fc);
   }
-  wait_vm(ntiles >= kNB ? (kNB - 1) * d_w : 0);
+  wait_vm(ntiles >= kNB ? (kNB - 2) * d_w : 0);
   barrier();
+  Frag<T> fr0[KS], fr1[KS];
   f32x16 acc0[NBW], acc1[NBW];
-  mfma_tile(std::integral_constant<int, 0>{}, acc0);
+  read_frags(std::integral_constant<int, 0>{}, fr0);
+  read_frags(std::integral_constant<int, 1>{}, fr1);
+  mfma_tile(fr0, acc0);
 
+  // Step k (U = k % 4): fragments of tile k+1 are in registers, tile k's
+  // MFMA results in the other accumulator set.
   int k = 0;
   auto step = [&](auto u_const) __attribute__((always_inline)) -> bool {
-    constexpr int U = decltype(u_const)::value;  // k % 4
+    constexpr int U = decltype(u_const)::value;
     f32x16 (&acc_cur)[NBW] = (U % 2 == 0) ? acc0 : acc1;
     f32x16 (&acc_nxt)[NBW] = (U % 2 == 0) ? acc1 : acc0;
-    // tile k+1 must be resident (it is read below even past the last tile:
-    // the results are then unused, but every wave must keep the barriers)
-    wait_vm(k + kNB - 1 < ntiles ? (kNB - 2) * d_w : 0);
+    Frag<T> (&fr_nxt)[KS] = (U % 2 == 0) ? fr1 : fr0;   // tile k+1
+    Frag<T> (&fr_new)[KS] = (U % 2 == 0) ? fr0 : fr1;   // <- tile k+2
+    // tile k+2 must be resident; this wave's loads of k+2 and k+3 may still be
+    // outstanding (k+3 only if it exists)
+    wait_vm(k + 3 < ntiles ? d_w : 0);
     barrier();
-    dma_tile(U, fc);                                  // tile k+4 -> buffer k % 4
+    dma_tile(U, fc);                                     // tile k+4 -> buffer k % 4
     fc = advance(fc);
-    mfma_tile(std::integral_constant<int, (U + 1) % kNB>{}, acc_nxt);
+    // Past the last tile these reads and MFMAs see stale buffers; their
+    // results are never used, and every wave keeps the same barrier count.
+    read_frags(std::integral_constant<int, (U + 2) % kNB>{}, fr_new);
+    mfma_tile(fr_nxt, acc_nxt);
     epilogue(acc_cur, cc);
     if (k + 1 >= ntiles) return true;
     cc = advance(cc);
@@ -677,12 +688,11 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   const dim3 grid((unsigned)(per_xcd * 8));
   const size_t lds = kTileBuffers * G::kBufPieces * sizeof(uint4) +
                      (kMaxDocsPerGroup + 1) * sizeof(int);
-  if (a.argmax)
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
-                       dim3(kTiledThreads), lds, st, a);
-  else
-    hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, false>), grid,
-                       dim3(kTiledThreads), lds, st, a);
+  // Score-only calls use the same kernel with argmax == nullptr: a variant
+  // without the index search needs more registers under this schedule and
+  // spills, which costs far more than the search.
+  hipLaunchKernelGGL((contrastive_tiled_kernel<T, KS, NBW, true>), grid,
+                     dim3(kTiledThreads), lds, st, a);
   }
 }
 
