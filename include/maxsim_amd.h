@@ -33,6 +33,7 @@
 #ifndef MAXSIM_AMD_H_
 #define MAXSIM_AMD_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -150,15 +151,27 @@ int maxsim_amd_contrastive_forward_with_argmax(
     const int32_t* document_offsets, int64_t num_documents, int64_t dim,
     float* scores, int32_t* argmax, void* stream);
 
+/* Bytes of device workspace that let maxsim_amd_contrastive_backward split
+ * the dqueries gather by document range (one range per XCD, partial sums
+ * added in a second pass).  0 for invalid sizes.  No counterpart in the
+ * reference, whose backward accumulates with global atomics instead. */
+size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
+                                                      int64_t dim);
+
 /* Replaces op `maxsim_contrastive_backward` (torch_binding.h:160-165,
  * maxsim.cu:1856-1920).  dscore [Nq, Nb], argmax [Nq, Nb, Lq] ->
- * dqueries [Nq, Lq, dim], ddocuments [total_d_tokens, dim]. */
+ * dqueries [Nq, Lq, dim], ddocuments [total_d_tokens, dim].
+ * `workspace` (device memory, 16-byte aligned for the vector path) of at
+ * least maxsim_amd_contrastive_backward_workspace_size() bytes selects the
+ * split dqueries pass; NULL or a smaller size selects the single-pass
+ * gather.  Both give the same result up to fp32 summation order. */
 int maxsim_amd_contrastive_backward(
     maxsim_dtype dtype, const float* dscore, const void* queries,
     int64_t num_queries, int64_t Lq, const void* documents,
     int64_t total_d_tokens, const int32_t* document_offsets,
     int64_t num_documents, const int32_t* argmax, int64_t dim,
-    float* dqueries, float* ddocuments, void* stream);
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -7,23 +7,29 @@
 //     dd[doc token j]    += g * q[query token i]
 //
 // Contrastive and padded layouts are done owner-computes, with no global
-// atomics and no zero-fill pass:
-//   * dq: one thread per (query token, 8-element slice) gathers the winning
-//     document row of every document it was scored against and accumulates
-//     in fp32 registers; each dq element is written exactly once.
-//   * dd (contrastive): one workgroup per (document, chunk of rows) keeps the
-//     chunk's fp32 gradient rows in LDS, scans the argmax entries of that
-//     document, and adds g * q for every entry that lands in the chunk with
-//     LDS atomics (pre-aggregation); the chunk is then written once.
+// atomics:
+//   * dq: a thread owns (query token, 8-element slice) and gathers the
+//     winning document row of every document the token was scored against,
+//     accumulating in fp32 registers.  Contrastive batches with a workspace
+//     split the documents into one range per XCD (so each XCD's L2 serves the
+//     gathers of its range) and add the eight partial sums in a second pass.
+//   * dd (contrastive): one workgroup per (document, part of the embedding
+//     dimension) buckets the document's argmax entries by target row in LDS
+//     (counting sort) and sums g * q over each row's bucket in registers; the
+//     dimension split keeps each XCD's slice of Q small enough for its L2.
+//     A row's bucket is summed in bucket order, which follows the order of
+//     the LDS atomics that filled it, so dd can differ between runs in the
+//     last bits (dq and padded dd are bitwise reproducible).
 //   * dd (padded): one wave per (query, candidate) document writes the
 //     document's rows once (zeros) and adds its <= Lq contributions in query
-//     token order, so the result is deterministic.
+//     token order.
 // Packed pairs can share queries and documents arbitrarily; there dq and dd
 // are zero-filled and accumulated with hardware fp32 global atomics.
 #include "maxsim_common.h"
 #include "maxsim_host.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace maxsim {
 
@@ -64,6 +70,21 @@ __device__ __forceinline__ void load8f(const typename T::storage* row, int k0,
       }
     }
   }
+}
+
+// Element e (0..7) of a raw fragment as fp32.
+__device__ __forceinline__ float frag_elem(const Frag<BF16>& f, int e) {
+  const uint32_t w = (e >> 1) == 0 ? f.v.x : (e >> 1) == 1 ? f.v.y : (e >> 1) == 2 ? f.v.z : f.v.w;
+  return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+__device__ __forceinline__ float frag_elem(const Frag<F16>& f, int e) {
+  const uint32_t w = (e >> 1) == 0 ? f.v.x : (e >> 1) == 1 ? f.v.y : (e >> 1) == 2 ? f.v.z : f.v.w;
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+__device__ __forceinline__ float frag_elem(const Frag<F32>& f, int e) {
+  const uint4 h = e < 4 ? f.lo : f.hi;
+  const int x = e & 3;
+  return __uint_as_float(x == 0 ? h.x : x == 1 ? h.y : x == 2 ? h.z : h.w);
 }
 
 __device__ __forceinline__ void store8f(float* row, int k0, int dim, bool vec,
@@ -209,16 +230,112 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 }
 
 // ---------------------------------------------------------------------------
-// dd, contrastive: one workgroup per document, LDS counting sort.
+// dq, contrastive, split by document range.
+//
+// gfx950 dispatches workgroup w to XCD w % 8, and each XCD has its own L2.
+// Range r = w % kXcds of the documents is therefore gathered only by the
+// workgroups of one XCD, so each XCD's L2 serves 1/8 of D instead of all of
+// it.  A thread owns (query row, 8-element slice, range) and walks the
+// range's documents U at a time (U winning rows in flight per lane), writing
+// its fp32 partial sum to ws[range]; dq_reduce_kernel adds the kXcds parts in
+// range order, so dq is bitwise reproducible.  U = 4 measured best at C5
+// (1: 229 us, 4: 200 us, 8: 271 us, 16: 387 us: larger U costs occupancy).
+// ---------------------------------------------------------------------------
+constexpr int kXcds = 8;
+constexpr int kDqBatch = 4;
+
+template <typename T, int U>
+__global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, bool vec, float* ws,
+                                                       int rows_per_group) {
+  using S = typename T::storage;
+  const int r = blockIdx.x % kXcds;
+  const int64_t grp = blockIdx.x / kXcds;
+  const int local = threadIdx.x / a.nslices;
+  if (local >= rows_per_group) return;
+  const int64_t row = grp * rows_per_group + local;
+  if (row >= a.rows) return;
+  const int sl = threadIdx.x - local * a.nslices;
+  const int k0 = sl * 8;
+  const int64_t qidx = row / a.lq;
+  const int i = (int)(row - qidx * a.lq);
+  const int64_t b_lo = a.nb * r / kXcds;
+  const int64_t b_hi = a.nb * (r + 1) / kXcds;
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int32_t* am = a.argmax + qidx * a.nb * a.lq + i;
+  const float* gq = a.dscore + qidx * a.nb;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t b0 = b_lo; b0 < b_hi; b0 += U) {
+    int64_t src[U];
+    float wt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t b = b0 + u;
+      src[u] = 0;
+      wt[u] = 0.0f;
+      if (b < b_hi) {
+        const int64_t s = a.doff[b], e = a.doff[b + 1];
+        const int j = am[b * a.lq];
+        if (s >= 0 && e > s && e <= a.total_d && j >= 0 && j < e - s) {
+          src[u] = s + j;
+          wt[u] = gq[b];
+        }
+      }
+    }
+    // raw 16-byte fragments; widened to fp32 only inside the FMAs
+    Frag<T> v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = load_frag<T>(D + src[u] * (int64_t)a.dim, k0, a.dim, vec);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int e2 = 0; e2 < 8; ++e2) acc[e2] = fmaf(wt[u], frag_elem(v[u], e2), acc[e2]);
+  }
+  store8f(ws + (int64_t)r * a.rows * a.dim + row * a.dim, k0, a.dim, vec, acc);
+}
+
+// dq[x] = sum over the kXcds partial buffers, in range order.
+__global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict__ ws,
+                                                        float* __restrict__ dq,
+                                                        int64_t n, bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n4 = vec ? n / 4 : 0;
+  for (int64_t x = t0; x < n4; x += stride) {
+    float4 s = reinterpret_cast<const float4*>(ws)[x];
+#pragma unroll
+    for (int r = 1; r < kXcds; ++r) {
+      const float4 v = reinterpret_cast<const float4*>(ws + r * n)[x];
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    reinterpret_cast<float4*>(dq)[x] = s;
+  }
+  for (int64_t x = n4 * 4 + t0; x < n; x += stride) {
+    float s = ws[x];
+#pragma unroll
+    for (int r = 1; r < kXcds; ++r) s += ws[r * n + x];
+    dq[x] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dd, contrastive: one workgroup per (document, part of the dimension), LDS
+// counting sort.
 //
 // Document b receives one entry per (query q, token i): row argmax[q, b, i].
 // The workgroup buckets those entries by target row in LDS (histogram,
-// exclusive scan, scatter of entry ids), then 16-lane groups each own one row
-// at a time and sum g[q, b] * q_row over the row's bucket in fp32 registers,
-// writing the gradient row once.  No floating-point atomics; every row of the
-// document is written (zeros for rows no entry points at).  Documents longer
-// than `rows_per_pass` rows and entry sets larger than `entries_per_pass` are
-// processed in passes (later entry passes add to the rows already written).
+// exclusive scan, scatter of entry ids), then groups of `group` lanes each
+// own one row at a time and sum g[q, b] * q_row over the row's bucket in fp32
+// registers, writing the gradient row once.  No floating-point atomics; every
+// row of the document is written (zeros for rows no entry points at).
+// Documents longer than `rows_per_pass` rows and entry sets larger than
+// `entries_per_pass` are processed in passes (later entry passes add to the
+// rows already written).
+//
+// Every document gathers rows from all of Q, so Q should stay in L2.  The
+// embedding dimension is split into `parts` (1, 2 or 4) slice ranges, part p
+// handled only by XCDs [p * 8 / parts, (p + 1) * 8 / parts) (workgroup w runs
+// on XCD w % 8): each XCD then gathers from 1 / parts of Q.  The bucketing
+// is repeated per part; its argmax reads are the cheaper side.
 // ---------------------------------------------------------------------------
 struct DdArgs {
   const float* dscore;
@@ -234,143 +351,197 @@ struct DdArgs {
   int nslices;
   int rows_per_pass;     // R: rows bucketed per pass (LDS: 2 * (R + 1) ints)
   int entries_per_pass;  // E: entry ids held per pass (LDS: E ints)
+  int parts;             // dimension parts (1, 2 or 4; divides kXcds)
+  int part_slices;       // 8-element slices per part (last part may hold fewer)
+  int group;             // lanes per row: power of two, <= 16, part_slices <= NS * group
 };
 
 constexpr int kDdThreads = 512;
-constexpr int kDdGroup = 16;                        // lanes per row
-constexpr int kDdGroups = kDdThreads / kDdGroup;    // rows in flight per workgroup
-constexpr int kDdMaxSlices = MAXSIM_AMD_MAX_DIM / 8 / kDdGroup;  // per lane
+constexpr int kDdMaxGroup = 16;
+constexpr int kDdBatch = 8;      // bucket entries gathered per step
+constexpr int kDdBlock = 32;     // bucket entries per block sum
 
-template <typename T>
-__global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a,
-                                                                    bool vec) {
+// x / d for 0 <= x < 2^24, d >= 1, from a float reciprocal: x is exact in
+// fp32 and the rounded product is within one of the quotient (exact for
+// d <= 2), so one remainder check gives the exact result.  Avoids the
+// branchy software integer division in the per-entry loops.
+__device__ __forceinline__ int div_small(int x, int d, float inv_d) {
+  int q = (int)((float)x * inv_d);
+  const int r = x - q * d;
+  q += (r >= d) ? 1 : 0;
+  q -= (r < 0) ? 1 : 0;
+  return q;
+}
+
+// Entries are processed in passes of whole queries when Lq <= E (qc queries
+// x Lq tokens), else in chunks of one query's tokens; pass-local entry x is
+// (query q0 + x / ic, token i0 + x % ic) with ic the tokens per query in the
+// pass, so its Q row is q0 * Lq + i0 + x in both cases.  The bucket holds
+// x | (x / ic) << 16 (x < 2^14), and the pass's dscore values are staged in
+// LDS, so the summation needs no division and no per-entry global index.
+template <typename T, bool VEC, int NS>
+__global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
   using S = typename T::storage;
   extern __shared__ int lds_i[];
   const int R = a.rows_per_pass;
+  const int E = a.entries_per_pass;
   int* start = lds_i;                 // [R + 1]
   int* cursor = start + (R + 1);      // [R + 1]
   int* ids = cursor + (R + 1);        // [E]
+  float* gst = reinterpret_cast<float*>(ids + E);  // [queries per pass]
 
-  const int64_t b = blockIdx.x;
+  // workgroup w -> XCD x = w % 8; part = x / (8 / parts); document
+  // b = (w / 8) * (8 / parts) + x % (8 / parts)
+  const int xcd = blockIdx.x % kXcds;
+  const int per_part = kXcds / a.parts;
+  const int part = xcd / per_part;
+  const int64_t b = (int64_t)(blockIdx.x / kXcds) * per_part + xcd % per_part;
+  if (b >= a.nb) return;
   const int64_t d0 = a.doff[b], d1 = a.doff[b + 1];
   if (d0 < 0 || d1 <= d0 || d1 > a.total_d) return;
   const int ld = (int)(d1 - d0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int grp = tid / kDdGroup;
-  const int gl = tid % kDdGroup;
+  const int G = a.group;
+  const int ngroups = kDdThreads / G;
+  const int grp = tid / G;
+  const int gl = tid - grp * G;
+  const int sl_lo = part * a.part_slices;
+  const int sl_hi = min(sl_lo + a.part_slices, a.nslices);
   const S* __restrict__ Q = static_cast<const S*>(a.q);
-  const int64_t n_entries = a.nq * a.lq;
   const int32_t* am_b = a.argmax + b * a.lq;   // entry (q, i) at am_b[q*nb*lq + i]
   const int64_t am_qstride = a.nb * a.lq;
+  const int tok_chunk = min(a.lq, E);
+  const int64_t qpp = (a.lq <= E) ? E / a.lq : 1;
 
   for (int r0 = 0; r0 < ld; r0 += R) {
     const int nrows = min(R, ld - r0);
-    for (int64_t e0 = 0; e0 < n_entries; e0 += a.entries_per_pass) {
-      const int ne = (int)min((int64_t)a.entries_per_pass, n_entries - e0);
-      for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
-      __syncthreads();
-      // 1. histogram of target rows
-      for (int x = tid; x < ne; x += kDdThreads) {
-        const int64_t e = e0 + x;
-        const int64_t qq = e / a.lq;
-        const int j = am_b[qq * am_qstride + (e - qq * a.lq)] - r0;
-        if (j >= 0 && j < nrows) atomicAdd(&start[j + 1], 1);
-      }
-      __syncthreads();
-      // 2. inclusive scan of start[1..nrows] by wave 0 (lane owns a run)
-      if (tid < 64) {
-        const int per = (nrows + 63) / 64;
-        const int lo = 1 + lane * per;
-        const int hi = min(lo + per, nrows + 1);
-        int run = 0;
-        for (int x = lo; x < hi; ++x) run += start[x];
-        int incl = run;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int v = __shfl_up(incl, off);
-          if (lane >= off) incl += v;
+    for (int64_t q0 = 0; q0 < a.nq; q0 += qpp) {
+      for (int i0 = 0; i0 < a.lq; i0 += tok_chunk) {
+        const int qc = (int)min(qpp, a.nq - q0);
+        const int ic = min(tok_chunk, a.lq - i0);
+        const int ne = qc * ic;
+        const float inv_ic = 1.0f / (float)ic;
+        const bool first = (q0 == 0 && i0 == 0);
+        const int32_t* am_p = am_b + q0 * am_qstride + i0;
+        const S* Qp = Q + (q0 * a.lq + i0) * (int64_t)a.dim;
+        for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
+        for (int x = tid; x < qc; x += kDdThreads) gst[x] = a.dscore[(q0 + x) * a.nb + b];
+        __syncthreads();
+        // 1. histogram of target rows
+        for (int x = tid; x < ne; x += kDdThreads) {
+          const int ql = div_small(x, ic, inv_ic);
+          const int j = am_p[ql * am_qstride + (x - ql * ic)] - r0;
+          if (j >= 0 && j < nrows) atomicAdd(&start[j + 1], 1);
         }
-        int acc = incl - run;
-        for (int x = lo; x < hi; ++x) {
-          acc += start[x];
-          start[x] = acc;
-        }
-      }
-      __syncthreads();
-      for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
-      __syncthreads();
-      // 3. scatter entry ids into their row buckets
-      for (int x = tid; x < ne; x += kDdThreads) {
-        const int64_t e = e0 + x;
-        const int64_t qq = e / a.lq;
-        const int j = am_b[qq * am_qstride + (e - qq * a.lq)] - r0;
-        if (j >= 0 && j < nrows) ids[atomicAdd(&cursor[j], 1)] = x;
-      }
-      __syncthreads();
-      // 4. per-row fp32 sums, one 16-lane group per row
-      for (int rr = grp; rr < nrows; rr += kDdGroups) {
-        float acc[kDdMaxSlices][8];
-        float* dst = a.dd + (d0 + r0 + rr) * (int64_t)a.dim;
+        __syncthreads();
+        // 2. inclusive scan of start[1..nrows] by wave 0 (lane owns a run)
+        if (tid < 64) {
+          const int per = (nrows + 63) / 64;
+          const int lo = 1 + lane * per;
+          const int hi = min(lo + per, nrows + 1);
+          int run = 0;
+          for (int x = lo; x < hi; ++x) run += start[x];
+          int incl = run;
 #pragma unroll
-        for (int u = 0; u < kDdMaxSlices; ++u) {
-          const int sl = gl + u * kDdGroup;
-          if (sl < a.nslices && e0 > 0) {
-            if (vec) {
-              const float4 x0 = *reinterpret_cast<const float4*>(dst + sl * 8);
-              const float4 x1 = *reinterpret_cast<const float4*>(dst + sl * 8 + 4);
-              acc[u][0] = x0.x; acc[u][1] = x0.y; acc[u][2] = x0.z; acc[u][3] = x0.w;
-              acc[u][4] = x1.x; acc[u][5] = x1.y; acc[u][6] = x1.z; acc[u][7] = x1.w;
+          for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off);
+            if (lane >= off) incl += v;
+          }
+          int acc = incl - run;
+          for (int x = lo; x < hi; ++x) {
+            acc += start[x];
+            start[x] = acc;
+          }
+        }
+        __syncthreads();
+        for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
+        __syncthreads();
+        // 3. scatter packed entry ids into their row buckets
+        for (int x = tid; x < ne; x += kDdThreads) {
+          const int ql = div_small(x, ic, inv_ic);
+          const int j = am_p[ql * am_qstride + (x - ql * ic)] - r0;
+          if (j >= 0 && j < nrows) ids[atomicAdd(&cursor[j], 1)] = x | (ql << 16);
+        }
+        __syncthreads();
+        // 4. per-row fp32 sums, one group of G lanes per row
+        for (int rr = grp; rr < nrows; rr += ngroups) {
+          float acc[NS][8];
+          float* dst = a.dd + (d0 + r0 + rr) * (int64_t)a.dim;
+#pragma unroll
+          for (int u = 0; u < NS; ++u) {
+            const int sl = sl_lo + gl + u * G;
+            if (sl < sl_hi && !first) {
+              load8f<F32>(dst, sl * 8, a.dim, VEC, acc[u]);
             } else {
 #pragma unroll
-              for (int k = 0; k < 8; ++k)
-                acc[u][k] = (sl * 8 + k < a.dim) ? dst[sl * 8 + k] : 0.0f;
-            }
-          } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc[u][k] = 0.0f;
-          }
-        }
-        const int s_end = start[rr + 1];
-        int s = start[rr];
-        // two entries per step keeps two row loads in flight per lane
-        for (; s + 1 < s_end; s += 2) {
-          const int64_t ea = e0 + ids[s], eb = e0 + ids[s + 1];
-          const float ga = a.dscore[(ea / a.lq) * a.nb + b];
-          const float gb = a.dscore[(eb / a.lq) * a.nb + b];
-#pragma unroll
-          for (int u = 0; u < kDdMaxSlices; ++u) {
-            const int sl = gl + u * kDdGroup;
-            if (sl < a.nslices) {
-              float va[8], vb[8];
-              load8f<T>(Q + ea * (int64_t)a.dim, sl * 8, a.dim, vec, va);
-              load8f<T>(Q + eb * (int64_t)a.dim, sl * 8, a.dim, vec, vb);
-#pragma unroll
-              for (int k = 0; k < 8; ++k) acc[u][k] = fmaf(gb, vb[k], fmaf(ga, va[k], acc[u][k]));
+              for (int k = 0; k < 8; ++k) acc[u][k] = 0.0f;
             }
           }
-        }
-        if (s < s_end) {
-          const int64_t ea = e0 + ids[s];
-          const float ga = a.dscore[(ea / a.lq) * a.nb + b];
+          const int s_end = start[rr + 1];
+          // Blocked summation: entries are added into a block sum, and every
+          // kDdBlock entries the block is added to the row sum.  A bucket can
+          // hold every entry of the batch (one-row documents, duplicated
+          // rows); plain sequential fp32 summation of n terms drifts like
+          // eps * n, blocking brings that to about eps * (kDdBlock + n / kDdBlock).
+          for (int s0 = start[rr]; s0 < s_end; s0 += kDdBlock) {
+            const int s1 = min(s0 + kDdBlock, s_end);
+            float blk[NS][8];
 #pragma unroll
-          for (int u = 0; u < kDdMaxSlices; ++u) {
-            const int sl = gl + u * kDdGroup;
-            if (sl < a.nslices) {
-              float va[8];
-              load8f<T>(Q + ea * (int64_t)a.dim, sl * 8, a.dim, vec, va);
+            for (int u = 0; u < NS; ++u)
 #pragma unroll
-              for (int k = 0; k < 8; ++k) acc[u][k] = fmaf(ga, va[k], acc[u][k]);
-            }
+              for (int e2 = 0; e2 < 8; ++e2) blk[u][e2] = 0.0f;
+            // kDdBatch entries per step keep that many row loads in flight per
+            // lane.  Full steps are unmasked; the last step of a block repeats
+            // its first entry past the block end and does not add it.
+            auto batch = [&](int s, auto masked) {
+              constexpr bool MASKED = decltype(masked)::value;
+              const S* row[kDdBatch];
+              float gx[kDdBatch];
+              bool ok[kDdBatch];
+#pragma unroll
+              for (int k = 0; k < kDdBatch; ++k) {
+                ok[k] = !MASKED || s + k < s1;
+                const int v = ids[ok[k] ? s + k : s];
+                row[k] = Qp + (v & 0xffff) * a.dim;
+                gx[k] = gst[v >> 16];
+              }
+#pragma unroll
+              for (int u = 0; u < NS; ++u) {
+                const int sl = sl_lo + gl + u * G;
+                if (sl < sl_hi) {
+                  // raw 16-byte fragments, widened to fp32 inside the FMAs
+                  Frag<T> v[kDdBatch];
+#pragma unroll
+                  for (int k = 0; k < kDdBatch; ++k)
+                    v[k] = load_frag<T>(row[k], sl * 8, a.dim, VEC);
+#pragma unroll
+                  for (int k = 0; k < kDdBatch; ++k) {
+#pragma unroll
+                    for (int e2 = 0; e2 < 8; ++e2) {
+                      const float t = fmaf(gx[k], frag_elem(v[k], e2), blk[u][e2]);
+                      blk[u][e2] = (!MASKED || ok[k]) ? t : blk[u][e2];
+                    }
+                  }
+                }
+              }
+            };
+            int s = s0;
+            for (; s + kDdBatch <= s1; s += kDdBatch) batch(s, std::false_type{});
+            if (s < s1) batch(s, std::true_type{});
+#pragma unroll
+            for (int u = 0; u < NS; ++u)
+#pragma unroll
+              for (int e2 = 0; e2 < 8; ++e2) acc[u][e2] += blk[u][e2];
+          }
+#pragma unroll
+          for (int u = 0; u < NS; ++u) {
+            const int sl = sl_lo + gl + u * G;
+            if (sl < sl_hi) store8f(dst, sl * 8, a.dim, VEC, acc[u]);
           }
         }
-#pragma unroll
-        for (int u = 0; u < kDdMaxSlices; ++u) {
-          const int sl = gl + u * kDdGroup;
-          if (sl < a.nslices) store8f(dst, sl * 8, a.dim, vec, acc[u]);
-        }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
 }
@@ -524,9 +695,41 @@ static void launch_dq(const DqArgs& a, bool vec, hipStream_t st) {
 }
 
 template <typename T>
+static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduce,
+                            hipStream_t st) {
+  const int rows_per_group = 256 / a.nslices;  // >= 8: dim <= 256
+  const int64_t n_groups = (a.rows + rows_per_group - 1) / rows_per_group;
+  hipLaunchKernelGGL((dq_split_kernel<T, kDqBatch>), dim3((unsigned)(n_groups * kXcds)),
+                     dim3(256), 0, st, a, vec, ws, rows_per_group);
+  const int64_t n = a.rows * a.dim;
+  const int64_t work = vec_reduce ? n / 4 : n;
+  const int64_t blocks = std::min<int64_t>((work + 255) / 256, 4096);
+  hipLaunchKernelGGL(dq_reduce_kernel, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256),
+                     0, st, ws, a.dq, n, vec_reduce);
+}
+
+template <typename T, bool VEC, int NS>
+static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st) {
+  const auto kern = dd_contrastive_kernel<T, VEC, NS>;
+  if (lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    (void)hipGetLastError();
+  }
+  const int64_t per_part = kXcds / a.parts;
+  const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
+}
+
+template <typename T>
 static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL(dd_contrastive_kernel<T>, dim3((unsigned)a.nb), dim3(kDdThreads), lds,
-                     st, a, vec);
+  const bool two = a.part_slices > a.group;
+  if (vec)
+    two ? launch_dd_contrastive_v<T, true, 2>(a, lds, st)
+        : launch_dd_contrastive_v<T, true, 1>(a, lds, st);
+  else
+    two ? launch_dd_contrastive_v<T, false, 2>(a, lds, st)
+        : launch_dd_contrastive_v<T, false, 1>(a, lds, st);
 }
 
 // Largest dynamic LDS allocation one workgroup may use on this device.
@@ -568,12 +771,19 @@ using namespace maxsim;
 
 extern "C" {
 
+size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
+                                                      int64_t dim) {
+  if (num_queries <= 0 || Lq <= 0 || dim <= 0 || dim > MAXSIM_AMD_MAX_DIM) return 0;
+  return (size_t)kXcds * (size_t)num_queries * (size_t)Lq * (size_t)dim * sizeof(float);
+}
+
 int maxsim_amd_contrastive_backward(
     maxsim_dtype dtype, const float* dscore, const void* queries,
     int64_t num_queries, int64_t Lq, const void* documents,
     int64_t total_d_tokens, const int32_t* document_offsets,
     int64_t num_documents, const int32_t* argmax, int64_t dim,
-    float* dqueries, float* ddocuments, void* stream) {
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
   clear_error();
   if (int e = check_dtype(dtype)) return e;
   if (num_queries < 0 || num_documents < 0 || total_d_tokens < 0)
@@ -613,8 +823,18 @@ int maxsim_amd_contrastive_backward(
   qa.nb = num_documents;
   qa.total_d = total_d_tokens;
   qa.padded = 0;
-  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, st);
-  if (int e = check_launch("dq_gather_kernel")) return e;
+  const size_t ws_need = maxsim_amd_contrastive_backward_workspace_size(num_queries, Lq, dim);
+  if (workspace && workspace_bytes >= ws_need) {
+    float* ws = static_cast<float*>(workspace);
+    const bool vec_ws = vec && aligned16b(workspace);
+    const bool vec_reduce = ((num_queries * Lq * dim) % 4 == 0) && aligned16b(workspace) &&
+                            aligned16b(dqueries);
+    MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, st);
+    if (int e = check_launch("dq_split_kernel")) return e;
+  } else {
+    MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, st);
+    if (int e = check_launch("dq_gather_kernel")) return e;
+  }
 
   // dd: one workgroup per document; every row of every valid document is
   // written.  LDS holds the row buckets (2 * (R + 1) ints) and up to E entry
@@ -632,22 +852,33 @@ int maxsim_amd_contrastive_backward(
   da.lq = (int)Lq;
   da.dim = (int)dim;
   da.nslices = nslices;
+  // dimension parts: the smallest of 1, 2, 4 that brings each XCD's share of
+  // Q to <= 4 MiB (one L2), never more parts than slices.  (At C5, Q = 4 MiB:
+  // one part measured 252 us against 260 us for two, whose L2 hit rate is
+  // higher but which bucket every document twice.)
+  const int64_t q_bytes = num_queries * Lq * dim * eb;
+  da.parts = 1;
+  while (da.parts < 4 && q_bytes / da.parts > (int64_t)(4 << 20) && da.parts * 2 <= nslices)
+    da.parts *= 2;
+  da.part_slices = (nslices + da.parts - 1) / da.parts;
+  da.group = 1;
+  while (da.group < kDdMaxGroup && da.group < da.part_slices) da.group *= 2;
   const size_t lds_cap = std::min<size_t>(max_lds_per_block(), 80 * 1024);
   da.rows_per_pass = 1024;
   const size_t bucket_bytes = 2 * (size_t)(da.rows_per_pass + 1) * sizeof(int);
   int64_t e_cap = (int64_t)((lds_cap - bucket_bytes) / sizeof(int));
-  if (e_cap > 16384) e_cap = 16384;
-  da.entries_per_pass = (int)std::min<int64_t>(e_cap, std::max<int64_t>(num_queries * Lq, 1));
-  const size_t lds = bucket_bytes + (size_t)da.entries_per_pass * sizeof(int);
-  if (lds > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<BF16>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<F16>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    (void)hipFuncSetAttribute((const void*)dd_contrastive_kernel<F32>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    (void)hipGetLastError();
+  if (e_cap > 16384) e_cap = 16384;  // pass-local entry ids stay < 2^24
+  // whole queries per pass when Lq fits (E ids + E / Lq staged dscore values),
+  // else one query's tokens in chunks of E (one staged value)
+  int64_t qpp = 1;
+  if (Lq <= e_cap) {
+    qpp = std::min<int64_t>(num_queries, e_cap / Lq);
+    while (qpp > 1 && qpp * Lq + qpp > e_cap) --qpp;
+    da.entries_per_pass = (int)(qpp * Lq);
+  } else {
+    da.entries_per_pass = (int)(e_cap - 1);
   }
+  const size_t lds = bucket_bytes + ((size_t)da.entries_per_pass + (size_t)qpp) * sizeof(int);
   MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, st);
   return check_launch("dd_contrastive_kernel");
 }

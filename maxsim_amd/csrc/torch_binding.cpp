@@ -366,10 +366,20 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
   Tensor dq = at::empty({Nq, Lq, c.q.size(2)}, f32_opts(c.q));
   Tensor dd = at::empty({c.d.size(0), c.d.size(1)}, f32_opts(c.q));
   c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
+  // With at least one document per XCD range, gather dq by range into a
+  // workspace of partial sums (see maxsim_amd_contrastive_backward_workspace_size).
+  Tensor ws;
+  size_t ws_bytes = 0;
+  if (Nb >= 8) {
+    ws_bytes = maxsim_amd_contrastive_backward_workspace_size(Nq, Lq, c.q.size(2));
+    if (ws_bytes > 0)
+      ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, f32_opts(c.q));
+  }
   check_status(maxsim_amd_contrastive_backward(
       to_dtype(c.q), g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(),
       c.d.size(0), c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(), c.q.size(2),
-      dq.data_ptr<float>(), dd.data_ptr<float>(), current_stream(c.q)));
+      dq.data_ptr<float>(), dd.data_ptr<float>(), ws.defined() ? ws.data_ptr() : nullptr,
+      ws.defined() ? ws_bytes : 0, current_stream(c.q)));
   return {dq, dd};
 }
 

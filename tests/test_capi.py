@@ -22,7 +22,7 @@ F32, F16, BF16 = 0, 1, 2
 
 def declared_functions() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(maxsim_amd_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(maxsim_amd_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 11, names
+    assert len(names) == 12, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,18 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 1
+    assert lib.maxsim_amd_abi_version() == 2
+
+
+def test_contrastive_backward_workspace_size(lib):
+    fn = lib.maxsim_amd_contrastive_backward_workspace_size
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    # eight fp32 partial copies of dq [Nq, Lq, dim]
+    assert fn(512, 32, 128) == 8 * 512 * 32 * 128 * 4
+    assert fn(3, 5, 7) == 8 * 3 * 5 * 7 * 4
+    for bad in [(0, 32, 128), (4, 0, 128), (4, 32, 0), (4, 32, 257), (-1, 32, 128)]:
+        assert fn(*bad) == 0
 
 
 I64 = ctypes.c_int64

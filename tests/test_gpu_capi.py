@@ -1,0 +1,87 @@
+"""The C ABI called directly (ctypes) on device buffers.
+
+The torch operators are one caller of libmaxsim_amd.so; these tests drive the
+same entry points the way a non-torch host would (raw device pointers, sizes,
+a stream handle) and check the choices the ABI leaves to its caller."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import pytest
+import torch
+
+import maxsim_amd
+from oracle import maxsim_oracle as oracle
+
+from ._helpers import DEVICE, GRAD_TOL, assert_close, make_contrastive, np64, npi
+
+pytestmark = pytest.mark.gpu
+
+LIB = Path(maxsim_amd.__file__).resolve().parent / "libmaxsim_amd.so"
+DT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+I64, P, SZ = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+
+
+@pytest.fixture(scope="module")
+def lib():
+    h = ctypes.CDLL(str(LIB))
+    h.maxsim_amd_last_error.restype = ctypes.c_char_p
+    h.maxsim_amd_contrastive_backward_workspace_size.restype = SZ
+    h.maxsim_amd_contrastive_backward_workspace_size.argtypes = [I64, I64, I64]
+    h.maxsim_amd_contrastive_backward.argtypes = [
+        ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P, SZ, P]
+    return h
+
+
+def _backward(lib, dscore, q, d, off, argmax, ws, ws_bytes):
+    Nq, Lq, dim = q.shape
+    dq = torch.full((Nq, Lq, dim), float("nan"), device=DEVICE)
+    dd = torch.full((d.shape[0], dim), float("nan"), device=DEVICE)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.maxsim_amd_contrastive_backward(
+        DT[q.dtype], dscore.data_ptr(), q.data_ptr(), Nq, Lq, d.data_ptr(), d.shape[0],
+        off.data_ptr(), off.numel() - 1, argmax.data_ptr(), dim, dq.data_ptr(), dd.data_ptr(),
+        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    assert rc == 0, lib.maxsim_amd_last_error()
+    torch.cuda.synchronize()
+    return dq, dd
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("d_lens", [[40] * 9, [3, 200, 1, 64, 17, 90, 5, 128, 33, 2, 70, 8, 16, 9]],
+                         ids=["Nb9", "Nb14-ragged"])
+def test_contrastive_backward_with_and_without_workspace(lib, dtype, d_lens):
+    """NULL workspace -> single-pass gather; a large enough workspace -> split
+    pass; a workspace one byte short -> single pass.  All match the oracle,
+    and the two dq paths differ only by fp32 summation order."""
+    Nq, Lq, dim = 6, 32, 128
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=21)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dscore = torch.randn(Nq, len(d_lens), generator=torch.Generator().manual_seed(2)).to(DEVICE)
+    need = lib.maxsim_amd_contrastive_backward_workspace_size(Nq, Lq, dim)
+    assert need == 8 * Nq * Lq * dim * 4
+    ws = torch.full((need // 4,), float("nan"), device=DEVICE)
+    dq0, dd0 = _backward(lib, dscore, q, d, off, argmax, None, 0)
+    dq1, dd1 = _backward(lib, dscore, q, d, off, argmax, ws, need)
+    dq2, dd2 = _backward(lib, dscore, q, d, off, argmax, ws, need - 1)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off), npi(argmax))
+    for dq, dd in [(dq0, dd0), (dq1, dd1), (dq2, dd2)]:
+        assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+        assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+    torch.testing.assert_close(dq0, dq1, rtol=1e-6, atol=1e-6)
+    # the single-pass gather is bitwise reproducible
+    assert torch.equal(dq0, dq2)
+
+
+def test_contrastive_backward_split_is_reproducible(lib):
+    q, d, off = make_contrastive(4, 32, 128, [50] * 16, torch.bfloat16, seed=5)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dscore = torch.randn(4, 16, generator=torch.Generator().manual_seed(8)).to(DEVICE)
+    need = lib.maxsim_amd_contrastive_backward_workspace_size(4, 32, 128)
+    ws = torch.empty(need // 4, device=DEVICE)
+    dq_a, _ = _backward(lib, dscore, q, d, off, argmax, ws, need)
+    ws.fill_(float("nan"))
+    dq_b, _ = _backward(lib, dscore, q, d, off, argmax, ws, need)
+    assert torch.equal(dq_a, dq_b)

@@ -76,6 +76,30 @@ def test_contrastive_backward(Nq, Lq, dim, d_lens, dtype):
     assert_close(dd, dd_ref, **GRAD_TOL[dtype])
 
 
+# Backward cases for the split dq pass (Nb >= 8: one document range per
+# XCD, eight partial sums) and for the dd kernel's dimension parts (Q larger
+# than 4 MiB: at 600 x 32 x 128, two parts for 16-bit and four for fp32).
+BWD_SPLIT = [
+    pytest.param(4, 32, 128, [40] * 8, id="Nb8-split"),
+    pytest.param(3, 16, 20, [5, 70, 1, 33, 9, 64, 17, 2, 40, 8, 3, 90, 12], id="Nb13-dim20"),
+    pytest.param(2, 32, 256, [65, 129, 7, 1, 300, 31, 16, 48, 90, 2, 77], id="Nb11-dim256"),
+    pytest.param(600, 32, 128, [64, 10, 200, 33, 1, 128, 90, 47, 300, 5], id="Nq600-dim-parts"),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
+@pytest.mark.parametrize("Nq,Lq,dim,d_lens", BWD_SPLIT)
+def test_contrastive_backward_split(Nq, Lq, dim, d_lens, dtype):
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=Nq + dim)
+    gen = torch.Generator().manual_seed(9)
+    dscore = torch.randn(Nq, len(d_lens), generator=gen).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq, dd = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off), npi(argmax))
+    assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda t: str(t).split(".")[-1])
 @pytest.mark.parametrize("d_lens", [[48, 48, 48], [47, 5, 33]])
 def test_contrastive_first_index_wins_on_ties(dtype, d_lens):
