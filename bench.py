@@ -40,6 +40,9 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--quick", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--profile-ops", action="store_true",
+                   help="run only the C5 operators (3x forward+argmax, 3x backward) and a "
+                        "1 GiB device copy, for rocprofv3 counter passes")
     return p.parse_args()
 
 
@@ -134,6 +137,26 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def profile_ops(torch, dev):
+    """C5 operators in isolation plus a plain copy of known size: the copy's
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters to bytes."""
+    from maxsim_amd._ops import ops
+
+    q, d, off, _ = make_c5(torch, dev)
+    nq = q.shape[0]
+    for _ in range(3):
+        scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    dscore = (torch.softmax(scores, dim=1) - torch.eye(nq, device=dev)) / nq
+    for _ in range(3):
+        ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_ops": "c5", "copy_bytes": src.numel() * 4}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -150,6 +173,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.profile_ops:
+        profile_ops(torch, dev)
+        return
     K, W = args.steps, args.warmup
     extra = {}
 

@@ -377,7 +377,7 @@ __device__ __forceinline__ int div_small(int x, int d, float inv_d) {
 // x Lq tokens), else in chunks of one query's tokens; pass-local entry x is
 // (query q0 + x / ic, token i0 + x % ic) with ic the tokens per query in the
 // pass, so its Q row is q0 * Lq + i0 + x in both cases.  The bucket holds
-// x | (x / ic) << 16 (x < 2^14), and the pass's dscore values are staged in
+// x | (x / ic) << 16 (x < 2^16), and the pass's dscore values are staged in
 // LDS, so the summation needs no division and no per-entry global index.
 template <typename T, bool VEC, int NS>
 __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
@@ -502,8 +502,8 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
 #pragma unroll
               for (int k = 0; k < kDdBatch; ++k) {
                 ok[k] = !MASKED || s + k < s1;
-                const int v = ids[ok[k] ? s + k : s];
-                row[k] = Qp + (v & 0xffff) * a.dim;
+                const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
+                row[k] = Qp + (int64_t)(v & 0xffffu) * a.dim;
                 gx[k] = gst[v >> 16];
               }
 #pragma unroll
@@ -867,7 +867,7 @@ int maxsim_amd_contrastive_backward(
   da.rows_per_pass = 1024;
   const size_t bucket_bytes = 2 * (size_t)(da.rows_per_pass + 1) * sizeof(int);
   int64_t e_cap = (int64_t)((lds_cap - bucket_bytes) / sizeof(int));
-  if (e_cap > 16384) e_cap = 16384;  // pass-local entry ids stay < 2^24
+  if (e_cap > 65535) e_cap = 65535;  // packed bucket ids hold x < 2^16
   // whole queries per pass when Lq fits (E ids + E / Lq staged dscore values),
   // else one query's tokens in chunks of E (one staged value)
   int64_t qpp = 1;

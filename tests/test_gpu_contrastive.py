@@ -84,6 +84,8 @@ BWD_SPLIT = [
     pytest.param(3, 16, 20, [5, 70, 1, 33, 9, 64, 17, 2, 40, 8, 3, 90, 12], id="Nb13-dim20"),
     pytest.param(2, 32, 256, [65, 129, 7, 1, 300, 31, 16, 48, 90, 2, 77], id="Nb11-dim256"),
     pytest.param(600, 32, 128, [64, 10, 200, 33, 1, 128, 90, 47, 300, 5], id="Nq600-dim-parts"),
+    # more query tokens than one dd entry pass holds: passes over token chunks
+    pytest.param(1, 20000, 8, [3, 17, 1, 40, 9, 2, 5, 11], id="Lq20000-token-chunks"),
 ]
 
 
