@@ -32,6 +32,13 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
+# HBM-side bytes per launch of the forward kernel at C5, from the two
+# rocprofv3 counter passes in profiles/c5_ops_hbm_traffic.md (FETCH_SIZE and
+# WRITE_SIZE per dispatch, each scaled by the reading for a 1 GiB copy:
+# x3.813 and x1.952).  Counters cannot be read from inside this process, so
+# the figure is the committed measurement, not a live one.
+FWD_TRAFFIC_BYTES_C5 = int((165436.6 * 3.813 + 33918.1 * 1.952) * 1024)
+
 
 def parse_args():
     p = argparse.ArgumentParser()
@@ -288,16 +295,18 @@ def main():
     if not args.no_cpu:
         from oracle import torch_baseline
 
-        cores = len(os.sched_getaffinity(0))
+        # the GPU box's CPU share is 16 threads whatever the affinity mask shows
+        cores = min(16, len(os.sched_getaffinity(0)))
         torch.set_num_threads(cores)
-        nsample = 16
+        nsample = 64
         qc = q[:nsample].float().cpu()
         dc, mask = torch_baseline.pad_documents(d.float().cpu(), lens)
         rows = torch.arange(nsample)
         log(f"CPU baseline: {nsample} of {nq} query rows x {nb} docs on {cores} threads")
-        torch_baseline.contrastive_step(qc, rows, dc, mask, nq)  # warmup
+        for _ in range(2):  # warmup
+            torch_baseline.contrastive_step(qc, rows, dc, mask, nq)
         times = []
-        for _ in range(3):
+        for _ in range(5):
             t0 = time.perf_counter()
             torch_baseline.contrastive_step(qc, rows, dc, mask, nq)
             times.append(time.perf_counter() - t0)
@@ -305,7 +314,7 @@ def main():
         cpu_tflops = (flops_fwd * nsample / nq) / t_sample / 1e12
         cpu = {"value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
                "sample": f"C5 fwd+CE+bwd for {nsample}/{nq} query rows against all {nb} docs "
-                         f"(fp32 einsum+max, -inf masked padding to Ld_max), median of 3 after 1 warmup; "
+                         f"(fp32 einsum+max, -inf masked padding to Ld_max), median of 5 after 2 warmups; "
                          f"{t_sample:.3f} s per sample step; host CPU: {cpu_model()}",
                "step_ms_extrapolated": round(t_sample * nq / nsample * 1e3, 1)}
         log(f"CPU baseline: {t_sample:.3f} s per sample -> {cpu_tflops:.4f} TFLOP/s")
@@ -330,7 +339,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "contrastive_tiled_kernel (forward + argmax)",
                      "achieved": round(fwd_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": FWD_TRAFFIC_BYTES_C5,
+                     "traffic_source": "profiles/c5_ops_hbm_traffic.md"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

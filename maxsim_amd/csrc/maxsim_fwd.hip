@@ -5,10 +5,11 @@
 //  * contrastive_tiled_kernel -- all-pairs scoring (reference K6/K7,
 //    maxsim.cu:1227-1595).  A workgroup of 8 waves holds up to 16 query
 //    blocks (32 tokens each) in registers and streams the 32-row tiles of a
-//    chunk of documents through double-buffered LDS, so each document tile is
-//    read from L2 once per 16 queries instead of once per pair.  The
-//    blockIdx -> (query group, doc chunk) map keeps all query groups of a doc
-//    chunk on one XCD so the chunk is fetched into that XCD's L2 once.
+//    chunk of documents through a ring of four LDS buffers filled by direct
+//    global->LDS loads, so each document tile is read from L2 once per 16
+//    queries instead of once per pair.  The blockIdx -> (query group, doc
+//    chunk) map keeps all query groups of a doc chunk on one XCD so the
+//    chunk is fetched into that XCD's L2 once.
 //
 //  * pair_kernel -- one wave per run of (query, document) pairs, document
 //    rows loaded straight from global memory into MFMA operand registers
