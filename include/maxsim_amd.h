@@ -85,10 +85,25 @@ int maxsim_amd_packed_forward_with_argmax(
     const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
     int64_t max_q_len, float* scores, int32_t* argmax, void* stream);
 
+/* Bytes of device workspace that let maxsim_amd_packed_backward group the
+ * pairs by query and by document on the device and compute each gradient
+ * row once, without floating-point atomics: 4 * (2 * num_queries + 1 +
+ * 2 * num_documents + 1 + 2 * num_pairs).  No counterpart in the reference,
+ * whose backward zero-fills the gradients and accumulates with atomics. */
+size_t maxsim_amd_packed_backward_workspace_size(int64_t num_queries, int64_t num_documents,
+                                                 int64_t num_pairs);
+
 /* Replaces op `maxsim_packed_backward` (torch_binding.h:112-121,
  * maxsim.cu:2201-2286).  dscore [num_pairs] fp32, argmax [num_pairs,
  * max_q_len] -> dqueries [total_q_tokens, dim], ddocuments [total_d_tokens,
- * dim], both fp32. */
+ * dim], both fp32.
+ * With `workspace` (device memory, 4-byte aligned) of at least
+ * maxsim_amd_packed_backward_workspace_size() bytes and max_q_len < 65536,
+ * the gradients are computed per query and per document, each row written
+ * once (rows before the first and after the last segment are zeroed); the
+ * offsets must then be non-decreasing, since rows of overlapping segments
+ * are owned twice.  NULL or a smaller workspace selects the zero-fill + fp32
+ * atomics path. */
 int maxsim_amd_packed_backward(
     maxsim_dtype dtype, const float* dscore, const void* queries,
     int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
@@ -96,7 +111,8 @@ int maxsim_amd_packed_backward(
     const int32_t* document_offsets, int64_t num_documents,
     const int32_t* pair_query_ids, const int32_t* pair_document_ids,
     int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
-    float* dqueries, float* ddocuments, void* stream);
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream);
 
 /* ---- Padded rerank ------------------------------------------------------ */
 

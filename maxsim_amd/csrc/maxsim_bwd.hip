@@ -666,6 +666,360 @@ __global__ __launch_bounds__(256) void packed_bwd_kernel(PackedBwdArgs a,
 }
 
 // ---------------------------------------------------------------------------
+// Packed, owner-computes (used when the caller provides a workspace).
+//
+// The pairs are grouped by query and by document on the device with a
+// counting sort (count, scan, scatter of pair ids; integer atomics only).
+// One workgroup per query then gathers its dq rows over the query's pairs,
+// and one workgroup per document accumulates its dd rows in LDS, a chunk of
+// rows at a time, and writes every row once: no zero-fill pass and no
+// floating-point atomics in global memory.  Rows of the outputs that lie in
+// no valid query / document segment are not written.
+//
+// Workspace (int32): qstart[nq + 1] qcur[nq] dstart[nd + 1] dcur[nd]
+//                    qlist[P] dlist[P]
+// ---------------------------------------------------------------------------
+struct PackedGroups {
+  int32_t* qstart;
+  int32_t* qcur;
+  int32_t* dstart;
+  int32_t* dcur;
+  int32_t* qlist;
+  int32_t* dlist;
+};
+
+// Pair p is routed only if its ids and both segments are valid (the rule of
+// packed_bwd_kernel).
+__device__ __forceinline__ bool packed_pair_ok(const PackedBwdArgs& a, int64_t p, int64_t& qi,
+                                               int64_t& di) {
+  qi = a.qids[p];
+  di = a.dids[p];
+  if (qi < 0 || qi >= a.nq || di < 0 || di >= a.nd) return false;
+  const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
+  const int64_t ds = a.doff[di], de = a.doff[di + 1];
+  if (qs < 0 || qe <= qs || qe > a.total_q || qe - qs > a.slots) return false;
+  if (ds < 0 || de <= ds || de > a.total_d) return false;
+  return true;
+}
+
+__global__ __launch_bounds__(256) void pair_count_kernel(PackedBwdArgs a, PackedGroups g) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < a.npairs; p += stride) {
+    int64_t qi, di;
+    if (!packed_pair_ok(a, p, qi, di)) continue;
+    atomicAdd(&g.qstart[qi + 1], 1);
+    atomicAdd(&g.dstart[di + 1], 1);
+  }
+}
+
+// Workgroup 0 turns qstart[0..nq] (qstart[0] = 0, qstart[x + 1] = count of
+// group x) into group starts by an inclusive scan, workgroup 1 does dstart;
+// the cursors start at the group starts.
+constexpr int kScanThreads = 1024;
+__global__ __launch_bounds__(kScanThreads) void group_scan_kernel(PackedGroups g, int64_t nq,
+                                                                  int64_t nd) {
+  __shared__ int wave_tot[kScanThreads / 64];
+  int32_t* v = blockIdx.x == 0 ? g.qstart : g.dstart;
+  int32_t* cur = blockIdx.x == 0 ? g.qcur : g.dcur;
+  const int64_t n = (blockIdx.x == 0 ? nq : nd) + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+  const int64_t lo = min((int64_t)tid * per, n), hi = min(lo + per, n);
+  int run = 0;
+  for (int64_t x = lo; x < hi; ++x) run += v[x];
+  int incl = run;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < kScanThreads / 64 ? wave_tot[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(w, off);
+      if (lane >= off) w += t;
+    }
+    if (lane < kScanThreads / 64) wave_tot[lane] = w;  // inclusive over waves
+  }
+  __syncthreads();
+  int acc = incl - run + (wave > 0 ? wave_tot[wave - 1] : 0);
+  for (int64_t x = lo; x < hi; ++x) {
+    acc += v[x];
+    v[x] = acc;
+    if (x < n - 1) cur[x] = acc;
+  }
+}
+
+__global__ __launch_bounds__(256) void pair_scatter_kernel(PackedBwdArgs a, PackedGroups g) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < a.npairs; p += stride) {
+    int64_t qi, di;
+    if (!packed_pair_ok(a, p, qi, di)) continue;
+    g.qlist[atomicAdd(&g.qcur[qi], 1)] = (int32_t)p;
+    g.dlist[atomicAdd(&g.dcur[di], 1)] = (int32_t)p;
+  }
+}
+
+constexpr int kGroupThreads = 256;
+constexpr int kPairStage = 256;  // pairs staged in LDS at a time
+
+// Zero the rows [0, off[0]) and [off[nseg], total) of a [total, dim] fp32
+// output: the rows before the first and after the last segment, which no
+// per-segment workgroup owns.
+__global__ __launch_bounds__(256) void zero_outside_kernel(float* out, const int32_t* off,
+                                                           int64_t nseg, int64_t total, int dim) {
+  const int64_t head = min(max((int64_t)off[0], (int64_t)0), total);
+  const int64_t tail = min(max((int64_t)off[nseg], head), total);
+  const int64_t n_head = head * dim, n_tail = (total - tail) * dim;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n_head + n_tail; x += stride)
+    out[x < n_head ? x : tail * dim + (x - n_head)] = 0.0f;
+}
+
+// dq: workgroup = (query qi, block of its tokens); thread = (token row,
+// 8-element slice).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs a,
+                                                                  PackedGroups g) {
+  using S = typename T::storage;
+  __shared__ int64_t st_ds[kPairStage];
+  __shared__ int32_t st_ld[kPairStage];
+  __shared__ int32_t st_p[kPairStage];
+  __shared__ float st_g[kPairStage];
+  const int64_t qi = blockIdx.x;
+  const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
+  if (qs < 0 || qe <= qs || qe > a.total_q) return;
+  const int lq = (int)(qe - qs);
+  const int tid = threadIdx.x;
+  const int rows_per_pass = kGroupThreads / a.nslices;
+  // token block of this workgroup (grid.y covers max_q_len)
+  const int i0 = blockIdx.y * rows_per_pass;
+  if (i0 >= lq) return;
+  const int local = tid / a.nslices;
+  const int sl = tid - local * a.nslices;
+  const bool active = local < rows_per_pass;
+  const int k0 = sl * 8;
+  const int k_lo = g.qstart[qi], k_hi = g.qstart[qi + 1];
+  const bool seg_ok = lq <= a.slots;
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  {
+    const int i = i0 + local;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c0 = k_lo; seg_ok && c0 < k_hi; c0 += kPairStage) {
+      const int nc = min(kPairStage, k_hi - c0);
+      __syncthreads();
+      if (tid < nc) {
+        const int p = g.qlist[c0 + tid];
+        const int64_t di = a.dids[p];
+        const int64_t ds = a.doff[di];
+        st_ds[tid] = ds;
+        st_ld[tid] = (int)(a.doff[di + 1] - ds);
+        st_p[tid] = p;
+        st_g[tid] = a.dscore[p];
+      }
+      __syncthreads();
+      if (!active || i >= lq) continue;
+      constexpr int U = 4;
+      for (int k = 0; k < nc; k += U) {
+        const S* src[U];
+        float w[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int kk = min(k + u, nc - 1);
+          const int j = a.argmax[(int64_t)st_p[kk] * a.slots + i];
+          ok[u] = (k + u < nc) && j >= 0 && j < st_ld[kk];
+          src[u] = D + (st_ds[kk] + (ok[u] ? j : 0)) * (int64_t)a.dim;
+          w[u] = st_g[kk];
+        }
+        Frag<T> v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = load_frag<T>(src[u], k0, a.dim, VEC);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float t = fmaf(w[u], frag_elem(v[u], e), acc[e]);
+            acc[e] = ok[u] ? t : acc[e];
+          }
+      }
+    }
+    if (active && i < lq) store8f(a.dq + (qs + i) * (int64_t)a.dim, k0, a.dim, VEC, acc);
+  }
+}
+
+// dd: workgroup = document di.  The document's entries -- (pair k of its
+// group, token i < Lq of that pair's query), target row argmax[p_k, i] -- are
+// bucketed by target row in LDS (histogram, scan, scatter: a counting sort);
+// then groups of G lanes each own one row at a time, sum g_k * q_row over the
+// row's bucket in fp32 registers (blocked sums, as in the contrastive dd) and
+// write the row once, zeros for rows no entry points at.  Entries are taken
+// in stages of nc pairs x tc tokens (nc * tc <= kPkEntries), documents longer
+// than kPkRows rows in row passes; later stages add to the rows written.
+constexpr int kPkRows = 2048;     // rows bucketed per pass
+constexpr int kPkEntries = 4096;  // entries per stage (bucket ids held in LDS)
+
+template <typename T, bool VEC, int NS>
+__global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs a,
+                                                                  PackedGroups g, int G) {
+  using S = typename T::storage;
+  __shared__ int start[kPkRows + 1];
+  __shared__ int cursor[kPkRows + 1];
+  __shared__ int ids[kPkEntries];
+  __shared__ int64_t st_qs[kPairStage];
+  __shared__ int32_t st_lq[kPairStage];
+  __shared__ int32_t st_p[kPairStage];
+  __shared__ float st_g[kPairStage];
+  const int64_t di = blockIdx.x;
+  const int64_t ds = a.doff[di], de = a.doff[di + 1];
+  if (ds < 0 || de <= ds || de > a.total_d) return;
+  const int ld = (int)(de - ds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int grp = tid / G, gl = tid - grp * G;
+  const int ngroups = kGroupThreads / G;
+  const int k_lo = g.dstart[di], k_hi = g.dstart[di + 1];
+  const int dim = a.dim;
+  const int tc = min(a.slots, kPkEntries);               // tokens per stage
+  const int stage_pairs = min(kPairStage, kPkEntries / tc);
+  const float inv_tc = 1.0f / (float)tc;
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const int sl_hi = a.nslices;
+
+  for (int r0 = 0; r0 < ld; r0 += kPkRows) {
+    const int nrows = min(kPkRows, ld - r0);
+    // at least one stage, so documents without pairs still write zero rows
+    int c0 = k_lo;
+    do {
+      const int nc = min(stage_pairs, k_hi - c0);
+      __syncthreads();
+      if (tid < nc) {
+        const int p = g.dlist[c0 + tid];
+        const int64_t qi = a.qids[p];
+        const int64_t qs = a.qoff[qi];
+        st_qs[tid] = qs;
+        st_lq[tid] = (int)(a.qoff[qi + 1] - qs);
+        st_p[tid] = p;
+        st_g[tid] = a.dscore[p];
+      }
+      for (int t0 = 0; t0 == 0 || t0 < a.slots; t0 += tc) {
+        const bool first = (c0 == k_lo && t0 == 0);
+        const int ne = nc * tc;
+        __syncthreads();
+        for (int x = tid; x <= nrows; x += kGroupThreads) start[x] = 0;
+        __syncthreads();
+        // 1. histogram of target rows
+        for (int e = tid; e < ne; e += kGroupThreads) {
+          const int k = div_small(e, tc, inv_tc);
+          const int i = t0 + e - k * tc;
+          if (i >= st_lq[k]) continue;
+          const int j = a.argmax[(int64_t)st_p[k] * a.slots + i] - r0;
+          if (j >= 0 && j < nrows && j + r0 < ld) atomicAdd(&start[j + 1], 1);
+        }
+        __syncthreads();
+        // 2. inclusive scan of start[1..nrows] by wave 0
+        if (tid < 64) {
+          const int per = (nrows + 63) / 64;
+          const int lo = 1 + lane * per;
+          const int hi = min(lo + per, nrows + 1);
+          int run = 0;
+          for (int x = lo; x < hi; ++x) run += start[x];
+          int incl = run;
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off);
+            if (lane >= off) incl += v;
+          }
+          int acc = incl - run;
+          for (int x = lo; x < hi; ++x) {
+            acc += start[x];
+            start[x] = acc;
+          }
+        }
+        __syncthreads();
+        for (int x = tid; x < nrows; x += kGroupThreads) cursor[x] = start[x];
+        __syncthreads();
+        // 3. scatter packed entry ids (e | k << 16) into their row buckets
+        for (int e = tid; e < ne; e += kGroupThreads) {
+          const int k = div_small(e, tc, inv_tc);
+          const int i = t0 + e - k * tc;
+          if (i >= st_lq[k]) continue;
+          const int j = a.argmax[(int64_t)st_p[k] * a.slots + i] - r0;
+          if (j >= 0 && j < nrows && j + r0 < ld) ids[atomicAdd(&cursor[j], 1)] = e | (k << 16);
+        }
+        __syncthreads();
+        // 4. per-row fp32 sums, one group of G lanes per row
+        for (int rr = grp; rr < nrows; rr += ngroups) {
+          float acc[NS][8];
+          float* dst = a.dd + (ds + r0 + rr) * (int64_t)dim;
+#pragma unroll
+          for (int u = 0; u < NS; ++u) {
+            const int sl = gl + u * G;
+            if (sl < sl_hi && !first) {
+              load8f<F32>(dst, sl * 8, dim, VEC, acc[u]);
+            } else {
+#pragma unroll
+              for (int x = 0; x < 8; ++x) acc[u][x] = 0.0f;
+            }
+          }
+          const int s_end = start[rr + 1];
+          for (int s0 = start[rr]; s0 < s_end; s0 += kDdBlock) {
+            const int s1 = min(s0 + kDdBlock, s_end);
+            float blk[NS][8];
+#pragma unroll
+            for (int u = 0; u < NS; ++u)
+#pragma unroll
+              for (int x = 0; x < 8; ++x) blk[u][x] = 0.0f;
+            for (int s = s0; s < s1; s += kDdBatch) {
+              const S* row[kDdBatch];
+              float gx[kDdBatch];
+              bool ok[kDdBatch];
+#pragma unroll
+              for (int k = 0; k < kDdBatch; ++k) {
+                ok[k] = s + k < s1;
+                const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
+                const int kk = (int)(v >> 16);
+                const int i = t0 + (int)(v & 0xffffu) - kk * tc;
+                row[k] = Q + (st_qs[kk] + i) * (int64_t)dim;
+                gx[k] = st_g[kk];
+              }
+#pragma unroll
+              for (int u = 0; u < NS; ++u) {
+                const int sl = gl + u * G;
+                if (sl < sl_hi) {
+                  Frag<T> v[kDdBatch];
+#pragma unroll
+                  for (int k = 0; k < kDdBatch; ++k) v[k] = load_frag<T>(row[k], sl * 8, dim, VEC);
+#pragma unroll
+                  for (int k = 0; k < kDdBatch; ++k)
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) {
+                      const float t = fmaf(gx[k], frag_elem(v[k], x), blk[u][x]);
+                      blk[u][x] = ok[k] ? t : blk[u][x];
+                    }
+                }
+              }
+            }
+#pragma unroll
+            for (int u = 0; u < NS; ++u)
+#pragma unroll
+              for (int x = 0; x < 8; ++x) acc[u][x] += blk[u][x];
+          }
+#pragma unroll
+          for (int u = 0; u < NS; ++u) {
+            const int sl = gl + u * G;
+            if (sl < sl_hi) store8f(dst, sl * 8, dim, VEC, acc[u]);
+          }
+        }
+      }
+      c0 += nc;
+    } while (c0 < k_hi);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
 static bool aligned16b(const void* p) {
@@ -746,6 +1100,33 @@ template <typename T>
 static void launch_dd_padded(const PaddedDdArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.npairs + 3) / 4));
   hipLaunchKernelGGL(dd_padded_kernel<T>, grid, dim3(256), 0, st, a);
+}
+
+template <typename T>
+static void launch_packed_grouped(const PackedBwdArgs& a, const PackedGroups& g, bool vec,
+                                  int G, hipStream_t st) {
+  if (a.nq > 0) {
+    const int rows_per_pass = kGroupThreads / a.nslices;
+    const dim3 grid((unsigned)a.nq, (unsigned)((a.slots + rows_per_pass - 1) / rows_per_pass));
+    if (vec)
+      hipLaunchKernelGGL((dq_packed_kernel<T, true>), grid, dim3(kGroupThreads), 0, st, a, g);
+    else
+      hipLaunchKernelGGL((dq_packed_kernel<T, false>), grid, dim3(kGroupThreads), 0, st, a, g);
+  }
+  if (a.nd > 0) {
+    const bool two = a.nslices > G;
+    const dim3 grid((unsigned)a.nd);
+    if (vec && two)
+      hipLaunchKernelGGL((dd_packed_kernel<T, true, 2>), grid, dim3(kGroupThreads), 0, st, a, g, G);
+    else if (vec)
+      hipLaunchKernelGGL((dd_packed_kernel<T, true, 1>), grid, dim3(kGroupThreads), 0, st, a, g, G);
+    else if (two)
+      hipLaunchKernelGGL((dd_packed_kernel<T, false, 2>), grid, dim3(kGroupThreads), 0, st, a, g,
+                         G);
+    else
+      hipLaunchKernelGGL((dd_packed_kernel<T, false, 1>), grid, dim3(kGroupThreads), 0, st, a, g,
+                         G);
+  }
 }
 
 template <typename T>
@@ -943,6 +1324,13 @@ int maxsim_amd_padded_backward(
   return check_launch("dd_padded_kernel");
 }
 
+size_t maxsim_amd_packed_backward_workspace_size(int64_t num_queries, int64_t num_documents,
+                                                 int64_t num_pairs) {
+  if (num_queries < 0 || num_documents < 0 || num_pairs < 0) return 0;
+  const int64_t ints = 2 * num_queries + 1 + 2 * num_documents + 1 + 2 * num_pairs;
+  return (size_t)ints * sizeof(int32_t);
+}
+
 int maxsim_amd_packed_backward(
     maxsim_dtype dtype, const float* dscore, const void* queries,
     int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
@@ -950,7 +1338,8 @@ int maxsim_amd_packed_backward(
     const int32_t* document_offsets, int64_t num_documents,
     const int32_t* pair_query_ids, const int32_t* pair_document_ids,
     int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
-    float* dqueries, float* ddocuments, void* stream) {
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
   clear_error();
   if (int e = check_dtype(dtype)) return e;
   if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
@@ -962,9 +1351,15 @@ int maxsim_amd_packed_backward(
   hipStream_t st = static_cast<hipStream_t>(stream);
   if ((total_q_tokens > 0 && !dqueries) || (total_d_tokens > 0 && !ddocuments))
     return fail(MAXSIM_ERR_INVALID, "null gradient pointer");
-  if (total_q_tokens > 0) launch_fill(dqueries, total_q_tokens * dim, st);
-  if (total_d_tokens > 0) launch_fill(ddocuments, total_d_tokens * dim, st);
-  if (int e = check_launch("fill_zero_kernel")) return e;
+  const size_t ws_need =
+      maxsim_amd_packed_backward_workspace_size(num_queries, num_documents, num_pairs);
+  const bool grouped = num_pairs > 0 && workspace && workspace_bytes >= ws_need &&
+                       max_q_len < (1 << 16) && num_pairs < INT32_MAX;
+  if (!grouped) {
+    if (total_q_tokens > 0) launch_fill(dqueries, total_q_tokens * dim, st);
+    if (total_d_tokens > 0) launch_fill(ddocuments, total_d_tokens * dim, st);
+    if (int e = check_launch("fill_zero_kernel")) return e;
+  }
   if (num_pairs == 0) return MAXSIM_OK;
   if (!dscore || !queries || !documents || !query_offsets || !document_offsets ||
       !pair_query_ids || !pair_document_ids || !argmax)
@@ -993,8 +1388,38 @@ int maxsim_amd_packed_backward(
   a.dim = (int)dim;
   a.nslices = nslices;
   a.lanes_per_tok = pow2_at_least(nslices < 64 ? nslices : 64);
-  MAXSIM_DISPATCH(dtype, launch_packed_bwd, a, vec, st);
-  return check_launch("packed_bwd_kernel");
+  if (!grouped) {
+    MAXSIM_DISPATCH(dtype, launch_packed_bwd, a, vec, st);
+    return check_launch("packed_bwd_kernel");
+  }
+  // group the pairs by query and by document (counting sort in the workspace)
+  int32_t* w = static_cast<int32_t*>(workspace);
+  PackedGroups g{};
+  g.qstart = w;
+  g.qcur = g.qstart + (num_queries + 1);
+  g.dstart = g.qcur + num_queries;
+  g.dcur = g.dstart + (num_documents + 1);
+  g.qlist = g.dcur + num_documents;
+  g.dlist = g.qlist + num_pairs;
+  // zero qstart..dstart (qcur is written by the scan); fill works on the bits
+  launch_fill(reinterpret_cast<float*>(g.qstart),
+              (num_queries + 1) + num_queries + (num_documents + 1), st);
+  const int64_t pb = std::min<int64_t>((num_pairs + 255) / 256, 2048);
+  hipLaunchKernelGGL(pair_count_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
+  hipLaunchKernelGGL(group_scan_kernel, dim3(2), dim3(kScanThreads), 0, st, g, num_queries,
+                     num_documents);
+  hipLaunchKernelGGL(pair_scatter_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
+  if (int e = check_launch("pair grouping kernels")) return e;
+  if (total_q_tokens > 0)
+    hipLaunchKernelGGL(zero_outside_kernel, dim3(64), dim3(256), 0, st, dqueries, query_offsets,
+                       num_queries, total_q_tokens, (int)dim);
+  if (total_d_tokens > 0)
+    hipLaunchKernelGGL(zero_outside_kernel, dim3(64), dim3(256), 0, st, ddocuments,
+                       document_offsets, num_documents, total_d_tokens, (int)dim);
+  const int G = pow2_at_least(nslices < 16 ? nslices : 16);  // lanes per dd row
+  const bool vec_g = vec && aligned16b(dqueries) && aligned16b(ddocuments);
+  MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, st);
+  return check_launch("dq_packed_kernel / dd_packed_kernel");
 }
 
 }  // extern "C"

@@ -197,12 +197,19 @@ std::tuple<Tensor, Tensor> maxsim_packed_backward(
   Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, f32_opts(p.q));
   Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, f32_opts(p.q));
   c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
+  // workspace for grouping the pairs by query and document on the device
+  // (see maxsim_amd_packed_backward_workspace_size)
+  const size_t ws_bytes =
+      maxsim_amd_packed_backward_workspace_size(p.qoff.numel() - 1, p.doff.numel() - 1, np);
+  Tensor ws = at::empty({(int64_t)((ws_bytes + 3) / 4)},
+                        p.q.options().dtype(at::kInt));
   check_status(maxsim_amd_packed_backward(
       to_dtype(p.q), g.data_ptr<float>(), p.q.data_ptr(), p.q.size(0),
       p.qoff.data_ptr<int32_t>(), p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0),
       p.doff.data_ptr<int32_t>(), p.doff.numel() - 1, p.qids.data_ptr<int32_t>(),
       p.dids.data_ptr<int32_t>(), np, am.data_ptr<int32_t>(), p.mql, p.q.size(1),
-      dq.data_ptr<float>(), dd.data_ptr<float>(), current_stream(p.q)));
+      dq.data_ptr<float>(), dd.data_ptr<float>(), ws.data_ptr(), ws_bytes,
+      current_stream(p.q)));
   return {dq, dd};
 }
 

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 12, names
+    assert len(names) == 13, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 2
+    assert lib.maxsim_amd_abi_version() == 3
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -61,6 +61,16 @@ def test_contrastive_backward_workspace_size(lib):
     assert fn(3, 5, 7) == 8 * 3 * 5 * 7 * 4
     for bad in [(0, 32, 128), (4, 0, 128), (4, 32, 0), (4, 32, 257), (-1, 32, 128)]:
         assert fn(*bad) == 0
+
+
+def test_packed_backward_workspace_size(lib):
+    fn = lib.maxsim_amd_packed_backward_workspace_size
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    # group starts + cursors for queries and documents, two pair lists (int32)
+    assert fn(512, 8192, 20000) == 4 * (2 * 512 + 1 + 2 * 8192 + 1 + 2 * 20000)
+    assert fn(0, 0, 0) == 8
+    assert fn(-1, 4, 4) == 0
 
 
 I64 = ctypes.c_int64

@@ -85,3 +85,41 @@ def test_contrastive_backward_split_is_reproducible(lib):
     ws.fill_(float("nan"))
     dq_b, _ = _backward(lib, dscore, q, d, off, argmax, ws, need)
     assert torch.equal(dq_a, dq_b)
+
+
+def test_packed_backward_with_and_without_workspace(lib):
+    """The grouped (workspace) and atomic (no workspace) packed backward paths
+    agree with the oracle and with each other."""
+    from ._helpers import make_packed
+
+    q, qoff, d, doff, qids, dids = make_packed(9, 17, 120, 128, (4, 40), (8, 400),
+                                               torch.bfloat16, seed=12)
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    mql = am.shape[1]
+    g = torch.randn(120, generator=torch.Generator().manual_seed(4)).to(DEVICE)
+    fn = lib.maxsim_amd_packed_backward
+    fn.argtypes = [ctypes.c_int, P, P, I64, P, I64, P, I64, P, I64, P, P, I64, P, I64, I64,
+                   P, P, P, SZ, P]
+    lib.maxsim_amd_packed_backward_workspace_size.restype = SZ
+    lib.maxsim_amd_packed_backward_workspace_size.argtypes = [I64, I64, I64]
+    need = lib.maxsim_amd_packed_backward_workspace_size(9, 17, 120)
+    ws = torch.full((need // 4 + 1,), -7, dtype=torch.int32, device=DEVICE)
+    out = []
+    for w, nbytes in [(None, 0), (ws, need), (ws, need - 1)]:
+        dq = torch.full((q.shape[0], 128), float("nan"), device=DEVICE)
+        dd = torch.full((d.shape[0], 128), float("nan"), device=DEVICE)
+        rc = fn(DT[q.dtype], g.data_ptr(), q.data_ptr(), q.shape[0], qoff.data_ptr(), 9,
+                d.data_ptr(), d.shape[0], doff.data_ptr(), 17, qids.data_ptr(), dids.data_ptr(), 120,
+                am.data_ptr(), mql, 128, dq.data_ptr(), dd.data_ptr(),
+                w.data_ptr() if w is not None else None, nbytes,
+                torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.maxsim_amd_last_error()
+        torch.cuda.synchronize()
+        out.append((dq, dd))
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), np64(q), npi(qoff), np64(d), npi(doff),
+                                            npi(qids), npi(dids), npi(am))
+    for dq, dd in out:
+        assert_close(dq, dq_ref, **GRAD_TOL[torch.bfloat16])
+        assert_close(dd, dd_ref, **GRAD_TOL[torch.bfloat16])
+    torch.testing.assert_close(out[0][0], out[1][0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(out[0][1], out[1][1], rtol=1e-5, atol=1e-5)

@@ -56,6 +56,47 @@ def test_packed_forward_argmax_backward(nq, nd, npairs, dim, qr, dr, dtype):
     assert_close(dd, dd_ref, **GRAD_TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_packed_backward_hot_query_and_document(dtype):
+    """One query and one document in 600 pairs each (more than one LDS stage
+    of the grouped backward), plus repeated identical pairs."""
+    q, qoff, d, doff, qids, dids = make_packed(7, 13, 900, 64, (4, 40), (8, 300), dtype, seed=77)
+    qids[:600] = 2
+    dids[300:900] = 5
+    qids[890:] = 1
+    dids[890:] = 1
+    qn, dn, qo, do = np64(q), np64(d), npi(qoff), npi(doff)
+    mql = int(np.diff(qo).max())
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    g = torch.randn(900, generator=torch.Generator().manual_seed(6)).to(DEVICE)
+    dq, dd = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, mql)
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), qn, qo, dn, do, npi(qids), npi(dids), npi(am))
+    assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+
+
+def test_packed_backward_op_zeroes_rows_outside_segments():
+    """The op called directly (no Python validation) with offsets that leave
+    rows before the first and after the last segment: those gradient rows are
+    zero, as with the reference's zero-filled outputs."""
+    gen = torch.Generator().manual_seed(3)
+    q = torch.randn(12, 32, generator=gen).to(DEVICE)
+    d = torch.randn(20, 32, generator=gen).to(DEVICE)
+    qoff = torch.tensor([2, 5, 9], dtype=torch.int32, device=DEVICE)
+    doff = torch.tensor([3, 10, 16], dtype=torch.int32, device=DEVICE)
+    qids = torch.tensor([0, 1, 1, 0], dtype=torch.int32, device=DEVICE)
+    dids = torch.tensor([1, 0, 1, 0], dtype=torch.int32, device=DEVICE)
+    s, am = ops.maxsim_packed_forward_with_argmax(q, qoff, d, doff, qids, dids, 4)
+    g = torch.randn(4, generator=gen).to(DEVICE)
+    dq, dd = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, 4)
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), np64(q), npi(qoff), np64(d), npi(doff),
+                                            npi(qids), npi(dids), npi(am))
+    assert_close(dq, dq_ref, **GRAD_TOL[torch.float32])
+    assert_close(dd, dd_ref, **GRAD_TOL[torch.float32])
+    assert torch.all(dq[:2] == 0) and torch.all(dq[9:] == 0)
+    assert torch.all(dd[:3] == 0) and torch.all(dd[16:] == 0)
+
+
 def test_packed_single_pair_single_token_closed_form():
     """test_correctness.py:39-50: 1 x 1 tokens -> score is the dot product."""
     q = torch.randn(1, 16, device=DEVICE)
