@@ -83,18 +83,21 @@ def make_c5(torch, dev, seed=0, nq=512, nb=512, lq=32, dim=128, lo=128, hi=1024,
             lens.tolist())
 
 
-def make_c3(torch, dev, seed=0, B=256, C=1000, lq=32, ld=300, dim=128):
+def make_c3(torch, dev, seed=0, B=256, C=1000, lq=32, ld=300, dim=128, only=None):
+    """C3 inputs; ``only`` = list of query indices generates just those
+    queries (bit-identical to the same rows of the full set)."""
     F = torch.nn.functional
     g = torch.Generator().manual_seed(seed)
     dlen = torch.randint(32, ld + 1, (B, C), generator=g, dtype=torch.int32)
-    q = torch.empty(B, lq, dim, dtype=torch.float16, device=dev)
-    d = torch.empty(B, C, ld, dim, dtype=torch.float16, device=dev)
-    for b in range(B):  # chunk-seeded so any query subset is reproducible
+    rows = list(range(B)) if only is None else list(only)
+    q = torch.empty(len(rows), lq, dim, dtype=torch.float16, device=dev)
+    d = torch.empty(len(rows), C, ld, dim, dtype=torch.float16, device=dev)
+    for k, b in enumerate(rows):  # chunk-seeded so any query subset is reproducible
         gb = torch.Generator(device=dev).manual_seed(seed * 100003 + b)
-        q[b] = F.normalize(torch.randn(lq, dim, generator=gb, device=dev), dim=-1).half()
-        d[b] = F.normalize(torch.randn(C, ld, dim, generator=gb, device=dev), dim=-1).half()
-    qlen = torch.full((B,), lq, dtype=torch.int32, device=dev)
-    return q, d, qlen, dlen.to(dev)
+        q[k] = F.normalize(torch.randn(lq, dim, generator=gb, device=dev), dim=-1).half()
+        d[k] = F.normalize(torch.randn(C, ld, dim, generator=gb, device=dev), dim=-1).half()
+    qlen = torch.full((len(rows),), lq, dtype=torch.int32, device=dev)
+    return q, d, qlen, dlen[rows].to(dev)
 
 
 def make_c4(torch, dev, seed=0, nq=512, nd=8192, npairs=20000, dim=128):
