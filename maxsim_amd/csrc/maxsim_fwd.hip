@@ -290,10 +290,12 @@ struct TileGeom {
   static constexpr int kBufPieces = kPieces;                // uint4 per buffer
 };
 
-// Position in the (document, tile) walk of a workgroup.
+// Position in the (document, tile) walk of a workgroup.  All fields are
+// wave-uniform 32-bit values (document offsets are int32), so the walk stays
+// in scalar registers.
 struct TileCursor {
-  int64_t b;      // document
-  int64_t row0;   // its first row
+  int b;          // document, relative to the workgroup's first
+  int row0;       // its first row
   int ld;         // its length (0 when past the end)
   int t;          // tile within the document
 };
@@ -349,17 +351,21 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     doff_lds[i] = a.doff[b_begin + i];
   __syncthreads();
 
-  auto doc_ok = [&](int64_t b, int64_t& s0, int& ld) {
-    const int64_t s = doff_lds[b - b_begin], e = doff_lds[b - b_begin + 1];
+  const int n_docs = (int)(b_end - b_begin);
+  // Offsets of local document bl (uniform: read back as scalars).
+  auto doc_ok = [&](int bl, int& s0, int& ld) {
+    const int s = __builtin_amdgcn_readfirstlane(doff_lds[bl]);
+    const int e = __builtin_amdgcn_readfirstlane(doff_lds[bl + 1]);
     s0 = s;
-    ld = (int)(e - s);
-    return (s >= 0) && (e > s) && (e <= a.total_d);
+    ld = e - s;
+    return (s >= 0) && (e > s) && ((int64_t)e <= a.total_d);
   };
   // Documents with invalid offsets: NaN score, zero argmax, never read.
-  for (int64_t b = b_begin; b < b_end; ++b) {
-    int64_t s0;
+  for (int bl = 0; bl < n_docs; ++bl) {
+    const int64_t b = b_begin + bl;
+    int s0;
     int ld;
-    if (doc_ok(b, s0, ld)) continue;
+    if (doc_ok(bl, s0, ld)) continue;
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
       const int64_t q = q_first + j / a.nblk;
@@ -369,14 +375,14 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
     }
   }
-  // First valid document at or after b (cursor at its tile 0).
-  auto seek = [&](int64_t b) -> TileCursor {
-    TileCursor cur{b_end, 0, 0, 0};
-    for (; b < b_end; ++b) {
-      int64_t s0;
+  // First valid document at or after local index bl (cursor at its tile 0).
+  auto seek = [&](int bl) -> TileCursor {
+    TileCursor cur{n_docs, 0, 0, 0};
+    for (; bl < n_docs; ++bl) {
+      int s0;
       int ld;
-      if (doc_ok(b, s0, ld)) {
-        cur.b = b;
+      if (doc_ok(bl, s0, ld)) {
+        cur.b = bl;
         cur.row0 = s0;
         cur.ld = ld;
         break;
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     return cur;
   };
   auto advance = [&](TileCursor cur) -> TileCursor {
-    if (cur.b >= b_end) return cur;
+    if (cur.b >= n_docs) return cur;
     if ((cur.t + 1) * kTileRows < cur.ld) {
       ++cur.t;
       return cur;
@@ -410,10 +416,10 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // registers are spent on global->LDS staging.  Vector-memory loads complete in issue order, so "at most N
   // loads outstanding" (s_waitcnt vmcnt(N)) identifies completed tiles.
   int ntiles = 0;
-  for (int64_t b = b_begin; b < b_end; ++b) {
-    int64_t s0;
+  for (int bl = 0; bl < n_docs; ++bl) {
+    int s0;
     int ld;
-    if (doc_ok(b, s0, ld)) ntiles += (ld + kTileRows - 1) / kTileRows;
+    if (doc_ok(bl, s0, ld)) ntiles += (ld + kTileRows - 1) / kTileRows;
   }
   if (ntiles == 0) return;
 
@@ -423,7 +429,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // wave w issues instructions j = w, w + 8, ...; d_w of them per tile
   const int d_w = (kDmaPerTile - wave + kTiledWaves - 1) / kTiledWaves;
   auto dma_tile = [&](int buf, const TileCursor& cur) __attribute__((always_inline)) {
-    if (cur.b >= b_end) return;
+    if (cur.b >= n_docs) return;
 #pragma unroll
     for (int i = 0; i < (kDmaPerTile + kTiledWaves - 1) / kTiledWaves; ++i) {
       const int j = wave + i * kTiledWaves;
@@ -526,8 +532,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
-          if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + cur.b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == 0) scores[q * a.nb + cur.b] = part_sum;
+          if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + b_begin + cur.b) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == 0) scores[q * a.nb + b_begin + cur.b] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
@@ -537,7 +543,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
 
   // ---- prologue: loads of tiles 0..3 issued; fragments of tiles 0 and 1
   // in registers; tile 0's MFMAs issued
-  TileCursor cc = seek(b_begin);      // tile k (epilogue)
+  TileCursor cc = seek(0);            // tile k (epilogue)
   TileCursor fc = cc;                 // next tile to load
 #pragma unroll
   for (int i = 0; i < kNB; ++i) {
@@ -567,13 +573,16 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     barrier();
     dma_tile(U, fc);                                     // tile k+4 -> buffer k % 4
     fc = advance(fc);
+    // The cursor walks read document offsets from LDS; doing both before
+    // this step's fragment reads keeps their waits off those reads.
+    const TileCursor cc_next = advance(cc);
     // Past the last tile these reads and MFMAs see stale buffers; their
     // results are never used, and every wave keeps the same barrier count.
     read_frags(std::integral_constant<int, (U + 2) % kNB>{}, fr_new);
     mfma_tile(fr_nxt, acc_nxt);
     epilogue(acc_cur, cc);
     if (k + 1 >= ntiles) return true;
-    cc = advance(cc);
+    cc = cc_next;
     ++k;
     return false;
   };
