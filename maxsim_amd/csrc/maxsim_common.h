@@ -162,22 +162,42 @@ __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
 }
 
 // Merge the two lane halves that own the same query token: larger value
-// wins, equal values keep the lower document index.
+// wins, equal values keep the lower document index.  v_permlane32_swap with
+// both operands equal leaves, in every lane l, the value of lane (l & 31)
+// in the first result and of lane (l & 31) + 32 in the second, so lanes c
+// and c + 32 compute the same merge without an LDS round trip.
 __device__ __forceinline__ void merge_halves(float& m, int& am) {
-  const float mo = __shfl_xor(m, 32);
-  const int ao = __shfl_xor(am, 32);
-  if (mo > m || (mo == m && ao < am)) {
-    m = mo;
-    am = ao;
-  }
+  const auto mv = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, m),
+                                                   __builtin_bit_cast(int, m), false, false);
+  const auto av = __builtin_amdgcn_permlane32_swap(am, am, false, false);
+  const float m_lo = __builtin_bit_cast(float, (int)mv[0]);
+  const float m_hi = __builtin_bit_cast(float, (int)mv[1]);
+  const int a_lo = (int)av[0], a_hi = (int)av[1];
+  const bool hi_wins = m_hi > m_lo || (m_hi == m_lo && a_hi < a_lo);
+  m = hi_wins ? m_hi : m_lo;
+  am = hi_wins ? a_hi : a_lo;
 }
 
-// Sum of `v` over the 32 lanes of each half (fixed butterfly order, so the
-// result is deterministic); every lane receives its half's sum.
+// DPP step: s + (s moved by the DPP control CTRL), rows outside ROW_MASK add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float s) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), CTRL, ROW_MASK, 0xF,
+                                            false);
+  return s + __builtin_bit_cast(float, t);
+}
+
+// Sum of `v` over the 32 lanes of each half with DPP moves (no LDS): pairs
+// (quad_perm [1,0,3,2]), quads ([2,3,0,1]), groups of 8 (row_half_mirror),
+// rows of 16 (row_mirror), then row 0's total broadcast into row 1 (and row
+// 2's into row 3).  The order is fixed, so the result is deterministic; it is
+// complete in lanes 16..31 and 48..63 (kHalfSumLane is one of them).
+constexpr int kHalfSumLane = 31;
 __device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v = dpp_add<0xB1, 0xF>(v);
+  v = dpp_add<0x4E, 0xF>(v);
+  v = dpp_add<0x141, 0xF>(v);
+  v = dpp_add<0x140, 0xF>(v);
+  return dpp_add<0x142, 0xA>(v);
 }
 
 }  // namespace maxsim

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
       for (int t = nblk * kTileCols + lane; t < a.slots; t += 64)
         a.argmax[p * a.slots + t] = 0;
     }
-    if (lane == 0) a.scores[p] = score;
+    if (lane == kHalfSumLane) a.scores[p] = score;
   }
 }
 
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
           if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + b_begin + cur.b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == 0) scores[q * a.nb + b_begin + cur.b] = part_sum;
+          if (part == a.nblk - 1 && lane == kHalfSumLane) scores[q * a.nb + b_begin + cur.b] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
