@@ -268,15 +268,21 @@ struct TiledArgs {
 // conservative wait for all loads in flight; the kernel orders these loads
 // itself (s_waitcnt vmcnt + s_barrier).  Loads complete in issue order, so
 // the compiler's own vmcnt waits stay correct (they can only get stricter).
-__device__ __forceinline__ void lds_dma16(const void* src, uint4* dst) {
-  // generic -> LDS address space gives the 32-bit LDS byte address
-  const uint32_t m0 = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) void*)dst);
+// 32-bit LDS byte address of an LDS pointer (generic -> LDS address space).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+
+// One wave instruction moving 16 bytes per lane from global memory
+// (uniform base + per-lane 32-bit byte offset) straight into LDS at
+// m0 + 16 * lane.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
   __asm__ __volatile__(
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
+      "global_load_lds_dwordx4 %0, %1"
       :
-      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(m0))
+      : "v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(m0))
       : "memory", "m0");
 }
 
@@ -428,19 +434,33 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   static_assert(G::kPieces % 64 == 0, "tile must be whole wave loads");
   // wave w issues instructions j = w, w + 8, ...; d_w of them per tile
   const int d_w = (kDmaPerTile - wave + kTiledWaves - 1) / kTiledWaves;
-  auto dma_tile = [&](int buf, const TileCursor& cur) __attribute__((always_inline)) {
-    if (cur.b >= n_docs) return;
+  // Per-lane part of each load slot, fixed for the whole walk: the slot's
+  // row within the tile and its byte offset within that row (swizzled
+  // piece); the LDS destination of wave instruction j is a constant.
+  constexpr int kDmaIters = (kDmaPerTile + kTiledWaves - 1) / kTiledWaves;
+  int slot_row[kDmaIters];
+  uint32_t slot_byte[kDmaIters];
 #pragma unroll
-    for (int i = 0; i < (kDmaPerTile + kTiledWaves - 1) / kTiledWaves; ++i) {
+  for (int i = 0; i < kDmaIters; ++i) {
+    const int slot = (wave + i * kTiledWaves) * 64 + lane;
+    const int r = slot / G::P;
+    slot_row[i] = r;
+    slot_byte[i] = (uint32_t)(((slot - r * G::P) ^ (r & G::SWZ)) * 16);
+  }
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(S);
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+  auto dma_tile = [&](auto buf_const, const TileCursor& cur) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_const)::value;
+    if (cur.b >= n_docs) return;
+    // uniform tile base; rows past the document end repeat its last row
+    const S* base = D + (int64_t)(cur.row0 + cur.t * kTileRows) * dim;
+    const int last = cur.ld - 1 - cur.t * kTileRows;
+#pragma unroll
+    for (int i = 0; i < kDmaIters; ++i) {
       const int j = wave + i * kTiledWaves;
-      if (j < kDmaPerTile) {
-        const int slot = j * 64 + lane;
-        const int r = slot / G::P;
-        const int pc = (slot - r * G::P) ^ (r & G::SWZ);
-        const int row = min(cur.t * kTileRows + r, cur.ld - 1);
-        const S* src = D + (cur.row0 + row) * (int64_t)dim + pc * G::kPieceElems;
-        lds_dma16(src, lds + buf * G::kBufPieces + j * 64);
-      }
+      if (j < kDmaPerTile)
+        lds_dma16(base, (uint32_t)min(slot_row[i], last) * row_bytes + slot_byte[i],
+                  lds_base + (uint32_t)((BUF * G::kBufPieces + j * 64) * sizeof(uint4)));
     }
   };
   // s_waitcnt vmcnt(n) for the runtime n in {0, 1, 2, 3, 4, 6}; other waits
@@ -545,11 +565,15 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // in registers; tile 0's MFMAs issued
   TileCursor cc = seek(0);            // tile k (epilogue)
   TileCursor fc = cc;                 // next tile to load
-#pragma unroll
-  for (int i = 0; i < kNB; ++i) {
-    dma_tile(i, fc);
-    fc = advance(fc);
-  }
+  static_assert(kNB == 4, "prologue issues four tile loads");
+  dma_tile(std::integral_constant<int, 0>{}, fc);
+  fc = advance(fc);
+  dma_tile(std::integral_constant<int, 1>{}, fc);
+  fc = advance(fc);
+  dma_tile(std::integral_constant<int, 2>{}, fc);
+  fc = advance(fc);
+  dma_tile(std::integral_constant<int, 3>{}, fc);
+  fc = advance(fc);
   wait_vm(ntiles >= kNB ? (kNB - 2) * d_w : 0);
   barrier();
   Frag<T> fr0[KS], fr1[KS];
@@ -571,7 +595,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     // outstanding (k+3 only if it exists)
     wait_vm(k + 3 < ntiles ? d_w : 0);
     barrier();
-    dma_tile(U, fc);                                     // tile k+4 -> buffer k % 4
+    dma_tile(u_const, fc);                               // tile k+4 -> buffer k % 4
     fc = advance(fc);
     // The cursor walks read document offsets from LDS; doing both before
     // this step's fragment reads keeps their waits off those reads.
