@@ -161,6 +161,43 @@ __device__ __forceinline__ void tile_update(const f32x16& acc, float& m,
   }
 }
 
+// Running max with the index search deferred to the end of the document.
+// Per tile: the tile max (max3 tree), and when it beats the running max, the
+// new max, the base row of that tile (`bt`) and a copy of the tile's 16
+// values (`best`) -- 27 VALU instructions, every select reading one mask.
+// best_row() then finds the first row of the best tile holding the max, once
+// per document.  Same result as tile_update<true>: strict `>` keeps the
+// earliest tile, the row search keeps the lowest row within it, and the max
+// is always one of the copied values (fmaxf returns one of its operands).
+__device__ __forceinline__ void tile_update_deferred(const f32x16& acc, float& m, int& bt,
+                                                     f32x16& best, int row_base) {
+  const float t0 = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
+  const float t1 = fmaxf(fmaxf(acc[3], acc[4]), acc[5]);
+  const float t2 = fmaxf(fmaxf(acc[6], acc[7]), acc[8]);
+  const float t3 = fmaxf(fmaxf(acc[9], acc[10]), acc[11]);
+  const float t4 = fmaxf(fmaxf(acc[12], acc[13]), acc[14]);
+  const float t5 = fmaxf(fmaxf(t0, t1), t2);
+  const float t6 = fmaxf(fmaxf(t3, t4), acc[15]);
+  const float tmax = fmaxf(t5, t6);
+  const bool upd = tmax > m;
+  m = upd ? tmax : m;
+  bt = upd ? row_base : bt;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) best[r] = upd ? acc[r] : best[r];
+}
+
+// Row index of the running max: bt (< 0 when no tile ever set it -> 0)
+// plus the offset of the first copied value equal to m.
+__device__ __forceinline__ int best_row(const f32x16& best, float m, int bt) {
+  bool eq[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) eq[r] = best[r] == m;
+  int off = 8 * (15 >> 2) + (15 & 3);
+#pragma unroll
+  for (int r = 14; r >= 0; --r) off = eq[r] ? (8 * (r >> 2) + (r & 3)) : off;
+  return bt < 0 ? 0 : bt + off;
+}
+
 // Merge the two lane halves that own the same query token: larger value
 // wins, equal values keep the lower document index.  v_permlane32_swap with
 // both operands equal leaves, in every lane l, the value of lane (l & 31)

@@ -126,7 +126,9 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
   const int lane = threadIdx.x & 63;
   const int c = lane & 31;
   const int h = lane >> 5;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform (readfirstlane says so): pair indices stay scalar
+  const int64_t wave =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t p_begin = wave * ppw;
   if (p_begin >= a.npairs) return;
   const int64_t p_end = min(p_begin + (int64_t)ppw, a.npairs);
@@ -229,15 +231,13 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
 // Workgroup = 8 waves.  Wave w holds NBW query blocks: queries
 // [q0 + w*qpw, q0 + (w+1)*qpw), each of nblk = ceil(Lq/32) blocks, with
 // qpw * nblk <= NBW.  The workgroup walks the 32-row tiles of its chunk of
-// documents in order.  Each tile is fetched from global memory into
-// registers four steps ahead, written to one of two LDS buffers two steps
-// ahead, and read by all 8 waves as MFMA A-operands one step ahead, so the
-// max/argmax epilogue of one tile runs while the MFMAs of the next are in
-// flight.  In LDS a tile is 32 rows of
-// 16-byte pieces; the piece index is XOR-swizzled with the row so the
-// operand reads (one row per lane) are bank-conflict free.  Requires
-// dim == KS*16 and 16-byte aligned rows (the host routes other shapes to
-// pair_kernel).
+// documents in order through a ring of four LDS buffers: tile k+4 is loaded
+// straight from global memory into LDS while tile k+2's operand fragments are
+// read into registers and tile k+1's MFMAs run, so the max/argmax epilogue of
+// tile k overlaps the MFMAs of tile k+1.  In LDS a tile is 32 rows of 16-byte
+// pieces; the piece index is XOR-swizzled with the row so the operand reads
+// (one row per lane) are bank-conflict free.  Requires dim == KS*16 and
+// 16-byte aligned rows (the host routes other shapes to pair_kernel).
 constexpr int kTiledWaves = 8;
 constexpr int kTiledThreads = kTiledWaves * 64;
 constexpr int kTileBuffers = 4;        // LDS tile ring
@@ -268,6 +268,14 @@ struct TiledArgs {
 // conservative wait for all loads in flight; the kernel orders these loads
 // itself (s_waitcnt vmcnt + s_barrier).  Loads complete in issue order, so
 // the compiler's own vmcnt waits stay correct (they can only get stricter).
+// The same value, opaque to the optimiser (an empty asm statement): address
+// arithmetic that depends on it cannot be hoisted out of the loop, where it
+// would keep 64-bit per-lane pointers live across the whole tile walk.
+__device__ __forceinline__ int opaque(int v) {
+  __asm__ __volatile__("" : "+v"(v));
+  return v;
+}
+
 // 32-bit LDS byte address of an LDS pointer (generic -> LDS address space).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
@@ -277,7 +285,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // (uniform base + per-lane 32-bit byte offset) straight into LDS at
 // m0 + 16 * lane.
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
+  // s_nop 4: the compiler does not check hazards inside inline asm; five
+  // wait states cover a VALU write (e.g. readfirstlane) of an SGPR this
+  // load reads as its base.  s_nop 0 after the m0 write covers M0 -> LDS DMA.
   __asm__ __volatile__(
+      "s_nop 4\n\t"
       "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1"
@@ -323,7 +335,9 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   const int dc = (int)(L / a.n_qg);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // wave-uniform; readfirstlane tells the compiler so, which keeps every
+  // query index and output address derived from it in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int c = lane & 31;
   const int h = lane >> 5;
@@ -521,16 +535,25 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
 
   float m[NBW];
   int am[NBW];
+  int bt[NBW];        // base row of the tile holding the running max (< 0: none)
+  f32x16 best[NBW];   // that tile's values (index search deferred to the doc end)
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
     m[j] = -__builtin_inff();
     am[j] = 0;
+    bt[j] = -1;
+    best[j] = f32x16{};
   }
   auto epilogue = [&](f32x16 (&acc)[NBW], const TileCursor& cur) __attribute__((always_inline)) {
     const int valid = cur.ld - cur.t * kTileRows;
     const int row_base = cur.t * kTileRows + 4 * h;
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) tile_update<ARGMAX>(acc[j], m[j], am[j], row_base);
+    for (int j = 0; j < NBW; ++j) {
+      if constexpr (ARGMAX)
+        tile_update_deferred(acc[j], m[j], bt[j], best[j], row_base);
+      else
+        tile_update<false>(acc[j], m[j], am[j], row_base);
+    }
     // Interleave the epilogue's VALU work and the operand reads for the tile
     // after next with the next tile's MFMAs, so one wave keeps the MFMA,
     // VALU and LDS pipes busy at once.
@@ -546,8 +569,9 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       for (int j = 0; j < NBW; ++j) {
         const int part = j % a.nblk;
         const int64_t q = q_first + j / a.nblk;
+        if constexpr (ARGMAX) am[j] = best_row(best[j], m[j], bt[j]);
         merge_halves(m[j], am[j]);
-        const int tok = part * kTileCols + c;
+        const int tok = part * kTileCols + opaque(c);
         const bool vtok = tok < a.lq;
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
@@ -557,6 +581,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
+        bt[j] = -1;
       }
     }
   };
