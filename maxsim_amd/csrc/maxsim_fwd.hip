@@ -119,9 +119,13 @@ __device__ __forceinline__ void write_invalid_pair(const FwdArgs& a, int64_t p,
 // QB query blocks (32 tokens each) are held in registers; queries longer than
 // 32*QB tokens are processed QB blocks at a time, re-streaming the document.
 // ---------------------------------------------------------------------------
-template <typename T, int KS, int QB, bool ARGMAX>
-__global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw,
-                                                   bool vec) {
+// VEC (rows are whole 16-byte fragments, 16-byte aligned) is a template
+// parameter: as a runtime flag, both load paths were compiled into the tile
+// loop, and the element-wise one's bounds checks drove the kernel into
+// scalar-register spills.
+template <typename T, int KS, int QB, bool ARGMAX, bool VEC>
+__global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
+  constexpr bool vec = VEC;
   using S = typename T::storage;
   const int lane = threadIdx.x & 63;
   const int c = lane & 31;
@@ -662,12 +666,14 @@ static bool aligned16(const void* p) {
 template <typename T, int KS, int QB>
 static void launch_pair_qb(const FwdArgs& a, int ppw, bool vec, dim3 grid,
                            hipStream_t st) {
-  if (a.argmax)
-    hipLaunchKernelGGL((pair_kernel<T, KS, QB, true>), grid, dim3(256), 0, st,
-                       a, ppw, vec);
+  if (a.argmax && vec)
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, true, true>), grid, dim3(256), 0, st, a, ppw);
+  else if (a.argmax)
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, true, false>), grid, dim3(256), 0, st, a, ppw);
+  else if (vec)
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, false, true>), grid, dim3(256), 0, st, a, ppw);
   else
-    hipLaunchKernelGGL((pair_kernel<T, KS, QB, false>), grid, dim3(256), 0,
-                       st, a, ppw, vec);
+    hipLaunchKernelGGL((pair_kernel<T, KS, QB, false, false>), grid, dim3(256), 0, st, a, ppw);
 }
 
 template <typename T, int KS>
