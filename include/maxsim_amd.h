@@ -189,6 +189,25 @@ int maxsim_amd_contrastive_backward(
     float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream);
 
+/* maxsim_amd_contrastive_backward with the gradients written in
+ * `grad_dtype`: MAXSIM_FLOAT32, or the input dtype, in which case each
+ * element is the fp32 sum rounded to nearest even -- bit for bit what
+ * casting the fp32 gradients would give.  No counterpart in the reference:
+ * its autograd Function (torch-ext/maxsim/__init__.py:947-953) returns the
+ * fp32 gradients and autograd casts them to the input dtype in a separate
+ * pass; writing the input dtype directly removes that pass and halves the
+ * document-gradient write.  A 16-bit grad_dtype needs the document gradient
+ * in a single pass over the entries (num_queries * (Lq + 1) up to 18,430 on
+ * gfx950); beyond that the call returns MAXSIM_ERR_UNSUPPORTED before
+ * launching anything, and the caller uses the fp32 form. */
+int maxsim_amd_contrastive_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore,
+    const void* queries, int64_t num_queries, int64_t Lq,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

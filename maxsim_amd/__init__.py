@@ -491,13 +491,15 @@ class _ContrastiveFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dscore):
+        # The reference returns the fp32 gradients and autograd casts them to
+        # the input dtype; the typed operator writes that rounding directly.
         q, d, offs, argmax = ctx.saved_tensors
-        dq, dd = ops.maxsim_contrastive_backward(
+        dq, dd = ops.maxsim_contrastive_backward_typed(
             dscore.contiguous().to(torch.float32), q, d, offs, argmax)
         return dq, dd, None
 
 
 def score_contrastive_train(queries, documents, document_offsets) -> torch.Tensor:
-    """Differentiable :func:`score_contrastive` (fp32 gradients)."""
+    """Differentiable :func:`score_contrastive` (gradients accumulated in fp32)."""
     _check_contrastive(queries, documents, document_offsets)
     return _ContrastiveFn.apply(queries, documents, document_offsets)

@@ -7,7 +7,8 @@ Produces, next to this file:
 * ``_maxsim_amd_torch.so`` -- the torch operator registrations
   (``torch_binding.cpp``), linked against ``libmaxsim_amd.so``.
 
-Run ``python -m maxsim_amd._build`` (or ``__graft_entry__.build()``).  The HIP
+Run ``python maxsim_amd/_build.py`` (or ``__graft_entry__.build()``); not as
+``python -m``, which would import the package and its previous build first.  The HIP
 objects are compiled in parallel; nothing is cached between runs.
 """
 

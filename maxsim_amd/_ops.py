@@ -3,7 +3,10 @@
 ``ops`` is ``torch.ops.maxsim_amd``: the nine operators of the reference's
 torch extension (torch-ext/torch_binding.cpp:7-90) with identical names,
 argument order and return arity, implemented by hand-written HIP kernels for
-gfx950 behind the C ABI in ``include/maxsim_amd.h``.
+gfx950 behind the C ABI in ``include/maxsim_amd.h``.  One more operator,
+``maxsim_contrastive_backward_typed``, is the contrastive backward with the
+gradients in the inputs' dtype; the autograd Function uses it so that torch
+does not cast fp32 gradients in a separate pass.
 
 Importing this module loads ``_maxsim_amd_torch.so`` (which pulls in
 ``libmaxsim_amd.so``).  There is no fallback: if the native build is missing
@@ -24,7 +27,7 @@ if not TORCH_BINDING.exists() or not NATIVE_LIB.exists():
     raise ImportError(
         "maxsim_amd native libraries are not built "
         f"({TORCH_BINDING.name}, {NATIVE_LIB.name} missing in {_HERE}); "
-        "run `python -m maxsim_amd._build` (needs hipcc for gfx950)"
+        "run `python maxsim_amd/_build.py` (needs hipcc for gfx950)"
     )
 
 if not hasattr(torch.ops.maxsim_amd, "maxsim_contrastive_forward"):
@@ -97,6 +100,11 @@ def _(queries, documents, document_offsets):
 @torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward")
 def _(dscore, queries, documents, document_offsets, argmax):
     return _f32(queries, queries.shape), _f32(documents, documents.shape)
+
+
+@torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward_typed")
+def _(dscore, queries, documents, document_offsets, argmax):
+    return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
 
 
 __all__ = ["ops", "NATIVE_LIB", "TORCH_BINDING"]

@@ -99,17 +99,62 @@ __device__ __forceinline__ void store8f(float* row, int k0, int dim, bool vec,
   }
 }
 
+// fp32 -> 16-bit gradient element, round to nearest even: torch's
+// float -> bfloat16 rule (NaN becomes the quiet NaN 0x7FC0) and the
+// hardware float -> half conversion under the default rounding mode, so a
+// gradient written here equals the fp32 gradient cast by torch.
+template <typename O>
+__device__ __forceinline__ uint16_t to_out16(float f) {
+  if constexpr (__is_same(O, BF16)) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)0x7fc0;
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  } else {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// Element `off` of a gradient buffer of output type O.
+template <typename O>
+__device__ __forceinline__ void* out_at(void* base, int64_t off) {
+  return static_cast<char*>(base) + off * O::bytes;
+}
+
+// 8 gradient elements in the output type O (F32, BF16 or F16).  With vec the
+// row is 16-byte aligned and holds all 8 (dim % 8 == 0).
+template <typename O>
+__device__ __forceinline__ void store8(void* row_v, int k0, int dim, bool vec, const float v[8]) {
+  if constexpr (O::bytes == 4) {
+    store8f(static_cast<float*>(row_v), k0, dim, vec, v);
+  } else {
+    uint16_t* row = static_cast<uint16_t*>(row_v);
+    if (vec) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = (uint32_t)to_out16<O>(v[2 * e]) | ((uint32_t)to_out16<O>(v[2 * e + 1]) << 16);
+      *reinterpret_cast<uint4*>(row + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (k0 + e < dim) row[k0 + e] = to_out16<O>(v[e]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Fill (used instead of hipMemsetAsync so the entry points stay capturable).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n,
-                                                        bool vec) {
-  const int64_t n4 = vec ? n / 4 : 0;
+// E is float or uint16_t (zero bits are +0 in every dtype).
+template <typename E>
+__global__ __launch_bounds__(256) void fill_zero_kernel(E* p, int64_t n, bool vec) {
+  constexpr int kPer = 16 / sizeof(E);
+  const int64_t nv = vec ? n / kPer : 0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
-    reinterpret_cast<float4*>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    p[i] = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride)
+    reinterpret_cast<uint4*>(p)[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (int64_t i = nv * kPer + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    p[i] = E(0);
 }
 
 // ---------------------------------------------------------------------------
@@ -123,7 +168,7 @@ struct DqArgs {
   const void* q;  // unused by the gather itself (kept for symmetry)
   const void* d;
   const int32_t* argmax;
-  float* dq;
+  void* dq;       // fp32, or the input's 16-bit type (contrastive only)
   int dim;
   int nslices;
   int64_t rows;   // total query rows (Nq*Lq or B*Lq_max)
@@ -140,7 +185,7 @@ struct DqArgs {
   int padded;
 };
 
-template <typename T>
+template <typename T, typename O>
 __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
   using S = typename T::storage;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -226,7 +271,7 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
       }
     }
   }
-  store8f(a.dq + row * a.dim, k0, a.dim, vec, acc);
+  store8<O>(out_at<O>(a.dq, row * a.dim), k0, a.dim, vec, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -293,9 +338,11 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, bool vec, float
   store8f(ws + (int64_t)r * a.rows * a.dim + row * a.dim, k0, a.dim, vec, acc);
 }
 
-// dq[x] = sum over the kXcds partial buffers, in range order.
+// dq[x] = sum over the kXcds partial buffers, in range order, written in
+// the output type O.
+template <typename O>
 __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict__ ws,
-                                                        float* __restrict__ dq,
+                                                        void* __restrict__ dq,
                                                         int64_t n, bool vec) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -307,13 +354,22 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict_
       const float4 v = reinterpret_cast<const float4*>(ws + r * n)[x];
       s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
-    reinterpret_cast<float4*>(dq)[x] = s;
+    if constexpr (O::bytes == 4) {
+      reinterpret_cast<float4*>(dq)[x] = s;
+    } else {
+      reinterpret_cast<uint2*>(dq)[x] =
+          make_uint2((uint32_t)to_out16<O>(s.x) | ((uint32_t)to_out16<O>(s.y) << 16),
+                     (uint32_t)to_out16<O>(s.z) | ((uint32_t)to_out16<O>(s.w) << 16));
+    }
   }
   for (int64_t x = n4 * 4 + t0; x < n; x += stride) {
     float s = ws[x];
 #pragma unroll
     for (int r = 1; r < kXcds; ++r) s += ws[r * n + x];
-    dq[x] = s;
+    if constexpr (O::bytes == 4)
+      static_cast<float*>(dq)[x] = s;
+    else
+      static_cast<uint16_t*>(dq)[x] = to_out16<O>(s);
   }
 }
 
@@ -342,7 +398,7 @@ struct DdArgs {
   const void* q;
   const int32_t* argmax;
   const int32_t* doff;
-  float* dd;
+  void* dd;              // fp32, or the input's 16-bit type (one entry pass only)
   int64_t nq;
   int64_t nb;
   int64_t total_d;
@@ -379,7 +435,11 @@ __device__ __forceinline__ int div_small(int x, int d, float inv_d) {
 // pass, so its Q row is q0 * Lq + i0 + x in both cases.  The bucket holds
 // x | (x / ic) << 16 (x < 2^16), and the pass's dscore values are staged in
 // LDS, so the summation needs no division and no per-entry global index.
-template <typename T, bool VEC, int NS>
+// The gradient is written in the output type O; a 16-bit O requires a single
+// entry pass (the host checks), since later passes add to the rows in fp32.
+// Rows before the first and after the last document are zeroed by part 0 of
+// the first and the last document.
+template <typename T, bool VEC, int NS, typename O>
 __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
   using S = typename T::storage;
   extern __shared__ int lds_i[];
@@ -397,6 +457,20 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
   const int part = xcd / per_part;
   const int64_t b = (int64_t)(blockIdx.x / kXcds) * per_part + xcd % per_part;
   if (b >= a.nb) return;
+  if (part == 0 && (b == 0 || b == a.nb - 1)) {
+    const int64_t head = min(max((int64_t)a.doff[0], (int64_t)0), a.total_d);
+    const int64_t tail = min(max((int64_t)a.doff[a.nb], head), a.total_d);
+    auto zero_rows = [&](int64_t lo, int64_t hi) {
+      for (int64_t x = lo * a.dim + threadIdx.x; x < hi * a.dim; x += kDdThreads) {
+        if constexpr (O::bytes == 4)
+          static_cast<float*>(a.dd)[x] = 0.0f;
+        else
+          static_cast<uint16_t*>(a.dd)[x] = 0;
+      }
+    };
+    if (b == 0) zero_rows(0, head);
+    if (b == a.nb - 1) zero_rows(tail, a.total_d);
+  }
   const int64_t d0 = a.doff[b], d1 = a.doff[b + 1];
   if (d0 < 0 || d1 <= d0 || d1 > a.total_d) return;
   const int ld = (int)(d1 - d0);
@@ -467,12 +541,12 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
         // 4. per-row fp32 sums, one group of G lanes per row
         for (int rr = grp; rr < nrows; rr += ngroups) {
           float acc[NS][8];
-          float* dst = a.dd + (d0 + r0 + rr) * (int64_t)a.dim;
+          void* dst = out_at<O>(a.dd, (d0 + r0 + rr) * (int64_t)a.dim);
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int sl = sl_lo + gl + u * G;
-            if (sl < sl_hi && !first) {
-              load8f<F32>(dst, sl * 8, a.dim, VEC, acc[u]);
+            if (O::bytes == 4 && sl < sl_hi && !first) {
+              load8f<F32>(static_cast<const float*>(dst), sl * 8, a.dim, VEC, acc[u]);
             } else {
 #pragma unroll
               for (int k = 0; k < 8; ++k) acc[u][k] = 0.0f;
@@ -537,7 +611,7 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int sl = sl_lo + gl + u * G;
-            if (sl < sl_hi) store8f(dst, sl * 8, a.dim, VEC, acc[u]);
+            if (sl < sl_hi) store8<O>(dst, sl * 8, a.dim, VEC, acc[u]);
           }
         }
         __syncthreads();
@@ -1032,24 +1106,37 @@ static int pow2_at_least(int x) {
   return p;
 }
 
-static void launch_fill(float* p, int64_t n, hipStream_t st) {
+template <typename E>
+static void launch_fill(E* p, int64_t n, hipStream_t st) {
   if (n <= 0) return;
-  int64_t blocks = (n / 4 + 255) / 256;
+  int64_t blocks = (n / (16 / (int64_t)sizeof(E)) + 255) / 256;
   if (blocks < 1) blocks = 1;
   if (blocks > 65535) blocks = 65535;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+  hipLaunchKernelGGL(fill_zero_kernel<E>, dim3((unsigned)blocks), dim3(256), 0, st,
                      p, n, aligned16b(p));
 }
 
+// n zero gradient elements of 4 (fp32) or 2 (16-bit) bytes
+static void launch_fill_grad(void* p, int64_t n, bool out16, hipStream_t st) {
+  if (out16)
+    launch_fill(static_cast<uint16_t*>(p), n, st);
+  else
+    launch_fill(static_cast<float*>(p), n, st);
+}
+
+// out16: gradients in the input's 16-bit type T instead of fp32.
 template <typename T>
-static void launch_dq(const DqArgs& a, bool vec, hipStream_t st) {
+static void launch_dq(const DqArgs& a, bool vec, bool out16, hipStream_t st) {
   const int64_t threads = a.rows * a.nslices;
   const dim3 grid((unsigned)((threads + 255) / 256));
-  hipLaunchKernelGGL(dq_gather_kernel<T>, grid, dim3(256), 0, st, a, vec);
+  if (out16)
+    hipLaunchKernelGGL((dq_gather_kernel<T, T>), grid, dim3(256), 0, st, a, vec);
+  else
+    hipLaunchKernelGGL((dq_gather_kernel<T, F32>), grid, dim3(256), 0, st, a, vec);
 }
 
 template <typename T>
-static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduce,
+static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduce, bool out16,
                             hipStream_t st) {
   const int rows_per_group = 256 / a.nslices;  // >= 8: dim <= 256
   const int64_t n_groups = (a.rows + rows_per_group - 1) / rows_per_group;
@@ -1057,14 +1144,16 @@ static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduc
                      dim3(256), 0, st, a, vec, ws, rows_per_group);
   const int64_t n = a.rows * a.dim;
   const int64_t work = vec_reduce ? n / 4 : n;
-  const int64_t blocks = std::min<int64_t>((work + 255) / 256, 4096);
-  hipLaunchKernelGGL(dq_reduce_kernel, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256),
-                     0, st, ws, a.dq, n, vec_reduce);
+  const dim3 grid((unsigned)std::max<int64_t>(std::min<int64_t>((work + 255) / 256, 4096), 1));
+  if (out16)
+    hipLaunchKernelGGL(dq_reduce_kernel<T>, grid, dim3(256), 0, st, ws, a.dq, n, vec_reduce);
+  else
+    hipLaunchKernelGGL(dq_reduce_kernel<F32>, grid, dim3(256), 0, st, ws, a.dq, n, vec_reduce);
 }
 
-template <typename T, bool VEC, int NS>
+template <typename T, bool VEC, int NS, typename O>
 static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st) {
-  const auto kern = dd_contrastive_kernel<T, VEC, NS>;
+  const auto kern = dd_contrastive_kernel<T, VEC, NS, O>;
   if (lds > 64 * 1024) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
@@ -1075,15 +1164,24 @@ static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st)
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
 }
 
-template <typename T>
-static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
+template <typename T, typename O>
+static void launch_dd_contrastive_o(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
   const bool two = a.part_slices > a.group;
   if (vec)
-    two ? launch_dd_contrastive_v<T, true, 2>(a, lds, st)
-        : launch_dd_contrastive_v<T, true, 1>(a, lds, st);
+    two ? launch_dd_contrastive_v<T, true, 2, O>(a, lds, st)
+        : launch_dd_contrastive_v<T, true, 1, O>(a, lds, st);
   else
-    two ? launch_dd_contrastive_v<T, false, 2>(a, lds, st)
-        : launch_dd_contrastive_v<T, false, 1>(a, lds, st);
+    two ? launch_dd_contrastive_v<T, false, 2, O>(a, lds, st)
+        : launch_dd_contrastive_v<T, false, 1, O>(a, lds, st);
+}
+
+template <typename T>
+static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, bool out16,
+                                  hipStream_t st) {
+  if (out16)
+    launch_dd_contrastive_o<T, T>(a, vec, lds, st);
+  else
+    launch_dd_contrastive_o<T, F32>(a, vec, lds, st);
 }
 
 // Largest dynamic LDS allocation one workgroup may use on this device.
@@ -1158,15 +1256,17 @@ size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64
   return (size_t)kXcds * (size_t)num_queries * (size_t)Lq * (size_t)dim * sizeof(float);
 }
 
-int maxsim_amd_contrastive_backward(
-    maxsim_dtype dtype, const float* dscore, const void* queries,
-    int64_t num_queries, int64_t Lq, const void* documents,
-    int64_t total_d_tokens, const int32_t* document_offsets,
-    int64_t num_documents, const int32_t* argmax, int64_t dim,
-    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+int maxsim_amd_contrastive_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t num_queries, int64_t Lq, const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents, const int32_t* argmax,
+    int64_t dim, void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream) {
   clear_error();
   if (int e = check_dtype(dtype)) return e;
+  if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
+    return fail(MAXSIM_ERR_INVALID, "grad_dtype must be MAXSIM_FLOAT32 or the input dtype");
+  const bool out16 = grad_dtype != MAXSIM_FLOAT32;
   if (num_queries < 0 || num_documents < 0 || total_d_tokens < 0)
     return fail(MAXSIM_ERR_INVALID, "negative size");
   if (Lq <= 0) return fail(MAXSIM_ERR_INVALID, "Lq must be > 0; got %lld", (long long)Lq);
@@ -1180,8 +1280,8 @@ int maxsim_amd_contrastive_backward(
   if (num_queries > 0 && !dqueries) return fail(MAXSIM_ERR_INVALID, "null dqueries");
   if (total_d_tokens > 0 && !ddocuments) return fail(MAXSIM_ERR_INVALID, "null ddocuments");
   if (num_queries == 0 || num_documents == 0) {
-    if (num_queries > 0) launch_fill(dqueries, num_queries * Lq * dim, st);
-    if (total_d_tokens > 0) launch_fill(ddocuments, total_d_tokens * dim, st);
+    if (num_queries > 0) launch_fill_grad(dqueries, num_queries * Lq * dim, out16, st);
+    if (total_d_tokens > 0) launch_fill_grad(ddocuments, total_d_tokens * dim, out16, st);
     return check_launch("fill_zero_kernel");
   }
   if (!dscore || !queries || !documents || !document_offsets || !argmax)
@@ -1189,35 +1289,7 @@ int maxsim_amd_contrastive_backward(
   if (total_d_tokens <= 0)
     return fail(MAXSIM_ERR_INVALID, "documents must not be empty when Nb > 0");
 
-  // dq
-  DqArgs qa{};
-  qa.dscore = dscore;
-  qa.q = queries;
-  qa.d = documents;
-  qa.argmax = argmax;
-  qa.dq = dqueries;
-  qa.dim = (int)dim;
-  qa.nslices = nslices;
-  qa.rows = num_queries * Lq;
-  qa.lq = (int)Lq;
-  qa.doff = document_offsets;
-  qa.nb = num_documents;
-  qa.total_d = total_d_tokens;
-  qa.padded = 0;
-  const size_t ws_need = maxsim_amd_contrastive_backward_workspace_size(num_queries, Lq, dim);
-  if (workspace && workspace_bytes >= ws_need) {
-    float* ws = static_cast<float*>(workspace);
-    const bool vec_ws = vec && aligned16b(workspace);
-    const bool vec_reduce = ((num_queries * Lq * dim) % 4 == 0) && aligned16b(workspace) &&
-                            aligned16b(dqueries);
-    MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, st);
-    if (int e = check_launch("dq_split_kernel")) return e;
-  } else {
-    MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, st);
-    if (int e = check_launch("dq_gather_kernel")) return e;
-  }
-
-  // dd: one workgroup per document; every row of every valid document is
+  // dd plan: one workgroup per document; every row of every valid document is
   // written.  LDS holds the row buckets (2 * (R + 1) ints) and up to E entry
   // ids; use up to 80 KB when the device allows, so C5-sized batches
   // (Nq * Lq = 16384 entries) need a single pass.
@@ -1259,9 +1331,57 @@ int maxsim_amd_contrastive_backward(
   } else {
     da.entries_per_pass = (int)(e_cap - 1);
   }
+  // later entry passes add to rows in fp32, so 16-bit output needs one pass
+  // (all queries at once, and no query split into token chunks)
+  if (out16 && (Lq > e_cap || qpp < num_queries))
+    return fail(MAXSIM_ERR_UNSUPPORTED,
+                "16-bit gradients need num_queries * Lq <= %lld entries; use fp32",
+                (long long)(e_cap * Lq / (Lq + 1)));
   const size_t lds = bucket_bytes + ((size_t)da.entries_per_pass + (size_t)qpp) * sizeof(int);
-  MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, st);
+
+  // dq
+  DqArgs qa{};
+  qa.dscore = dscore;
+  qa.q = queries;
+  qa.d = documents;
+  qa.argmax = argmax;
+  qa.dq = dqueries;
+  qa.dim = (int)dim;
+  qa.nslices = nslices;
+  qa.rows = num_queries * Lq;
+  qa.lq = (int)Lq;
+  qa.doff = document_offsets;
+  qa.nb = num_documents;
+  qa.total_d = total_d_tokens;
+  qa.padded = 0;
+  const size_t ws_need = maxsim_amd_contrastive_backward_workspace_size(num_queries, Lq, dim);
+  if (workspace && workspace_bytes >= ws_need) {
+    float* ws = static_cast<float*>(workspace);
+    const bool vec_ws = vec && aligned16b(workspace);
+    const bool vec_reduce = ((num_queries * Lq * dim) % 4 == 0) && aligned16b(workspace) &&
+                            aligned16b(dqueries);
+    MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, out16, st);
+    if (int e = check_launch("dq_split_kernel")) return e;
+  } else {
+    MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
+    if (int e = check_launch("dq_gather_kernel")) return e;
+  }
+
+  MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, out16, st);
   return check_launch("dd_contrastive_kernel");
+}
+
+int maxsim_amd_contrastive_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    int64_t num_queries, int64_t Lq, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* argmax, int64_t dim,
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  return maxsim_amd_contrastive_backward_typed(
+      dtype, MAXSIM_FLOAT32, dscore, queries, num_queries, Lq, documents, total_d_tokens,
+      document_offsets, num_documents, argmax, dim, dqueries, ddocuments, workspace,
+      workspace_bytes, stream);
 }
 
 int maxsim_amd_padded_backward(
@@ -1305,7 +1425,7 @@ int maxsim_amd_padded_backward(
   qa.ncand = num_candidates;
   qa.ld_max = (int)Ld_max;
   qa.padded = 1;
-  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, st);
+  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, false, st);
   if (int e = check_launch("dq_gather_kernel")) return e;
 
   PaddedDdArgs da{};

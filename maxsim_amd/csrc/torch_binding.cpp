@@ -357,9 +357,12 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_forward_with_argmax(
   return {scores, argmax};
 }
 
-std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
+// grads_in_input_dtype: write the gradients in the inputs' dtype (the C ABI's
+// typed entry point, rounding to nearest even like a cast); when the shapes
+// need the fp32 path, compute in fp32 and cast.
+std::tuple<Tensor, Tensor> contrastive_backward_impl(
     Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
-    Tensor argmax) {
+    Tensor argmax, bool grads_in_input_dtype) {
   Contrastive c = prep_contrastive(queries, documents, document_offsets);
   const int64_t Nq = c.q.size(0), Lq = c.q.size(1), Nb = c.off.numel() - 1;
   TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
@@ -370,8 +373,6 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
   TORCH_CHECK(argmax.numel() == Nq * Nb * Lq, "argmax must be [Nq, Nb, Lq]");
   Tensor g = dscore.contiguous();
   Tensor am = argmax.contiguous();
-  Tensor dq = at::empty({Nq, Lq, c.q.size(2)}, f32_opts(c.q));
-  Tensor dd = at::empty({c.d.size(0), c.d.size(1)}, f32_opts(c.q));
   c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
   // With at least one document per XCD range, gather dq by range into a
   // workspace of partial sums (see maxsim_amd_contrastive_backward_workspace_size).
@@ -382,12 +383,42 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
     if (ws_bytes > 0)
       ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, f32_opts(c.q));
   }
-  check_status(maxsim_amd_contrastive_backward(
-      to_dtype(c.q), g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(),
-      c.d.size(0), c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(), c.q.size(2),
-      dq.data_ptr<float>(), dd.data_ptr<float>(), ws.defined() ? ws.data_ptr() : nullptr,
-      ws.defined() ? ws_bytes : 0, current_stream(c.q)));
+  const maxsim_dtype dt = to_dtype(c.q);
+  auto run = [&](maxsim_dtype grad_dt, const at::TensorOptions& opts) {
+    Tensor dq = at::empty({Nq, Lq, c.q.size(2)}, opts);
+    Tensor dd = at::empty({c.d.size(0), c.d.size(1)}, opts);
+    const int rc = maxsim_amd_contrastive_backward_typed(
+        dt, grad_dt, g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(), c.d.size(0),
+        c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(), c.q.size(2), dq.data_ptr(),
+        dd.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws_bytes : 0,
+        current_stream(c.q));
+    return std::make_tuple(rc, dq, dd);
+  };
+  if (grads_in_input_dtype && dt != MAXSIM_FLOAT32) {
+    auto [rc, dq, dd] = run(dt, c.q.options());
+    if (rc == MAXSIM_OK) return {dq, dd};
+    // ERR_UNSUPPORTED is returned before any launch; fall through to fp32
+    TORCH_CHECK(rc == MAXSIM_ERR_UNSUPPORTED, "maxsim_amd: ", maxsim_amd_last_error());
+  }
+  auto [rc, dq, dd] = run(MAXSIM_FLOAT32, f32_opts(c.q));
+  check_status(rc);
+  if (grads_in_input_dtype && dt != MAXSIM_FLOAT32)
+    return {dq.to(c.q.scalar_type()), dd.to(c.q.scalar_type())};
   return {dq, dd};
+}
+
+std::tuple<Tensor, Tensor> maxsim_contrastive_backward(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
+    Tensor argmax) {
+  return contrastive_backward_impl(dscore, queries, documents, document_offsets, argmax, false);
+}
+
+// Not one of the reference's operators: the autograd Function's backward,
+// with gradients in the inputs' dtype.
+std::tuple<Tensor, Tensor> maxsim_contrastive_backward_typed(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
+    Tensor argmax) {
+  return contrastive_backward_impl(dscore, queries, documents, document_offsets, argmax, true);
 }
 
 }  // namespace
@@ -416,6 +447,9 @@ TORCH_LIBRARY(maxsim_amd, m) {
         "Tensor document_offsets) -> (Tensor, Tensor)");
   m.def("maxsim_contrastive_backward(Tensor dscore, Tensor queries, Tensor documents, "
         "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
+  // not in the reference: gradients in the inputs' dtype (used by autograd)
+  m.def("maxsim_contrastive_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
+        "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
@@ -429,4 +463,5 @@ TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
   m.impl("maxsim_contrastive_forward_with_argmax",
          &maxsim_contrastive_forward_with_argmax);
   m.impl("maxsim_contrastive_backward", &maxsim_contrastive_backward);
+  m.impl("maxsim_contrastive_backward_typed", &maxsim_contrastive_backward_typed);
 }

@@ -28,7 +28,7 @@ def declared_functions() -> list[str]:
 @pytest.fixture(scope="module")
 def lib():
     if not LIB.exists():
-        pytest.fail(f"{LIB} is not built; run python -m maxsim_amd._build")
+        pytest.fail(f"{LIB} is not built; run python maxsim_amd/_build.py")
     handle = ctypes.CDLL(str(LIB))
     handle.maxsim_amd_last_error.restype = ctypes.c_char_p
     return handle
@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 13, names
+    assert len(names) == 14, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 3
+    assert lib.maxsim_amd_abi_version() == 4
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -135,3 +135,27 @@ def test_backward_rejects_null_grads(lib):
     one = P(1)
     assert fn(BF16, one, one, one, one, one, one, 2, 3, 4, 8, 64, None, one, None) == INVALID
     assert b"null" in lib.maxsim_amd_last_error()
+
+
+def _typed_backward(lib, dtype=BF16, grad_dtype=BF16, nq=2, lq=16, nb=2, dim=64):
+    fn = lib.maxsim_amd_contrastive_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P,
+                   ctypes.c_size_t, P]
+    one = P(16)
+    return fn(dtype, grad_dtype, one, one, nq, lq, one, 64, one, nb, one, dim, one, one, None, 0,
+              None)
+
+
+def test_typed_backward_rejects_a_third_grad_dtype(lib):
+    # gradients are fp32 or the input dtype, nothing else
+    assert _typed_backward(lib, dtype=BF16, grad_dtype=F16) == INVALID
+    assert b"grad_dtype" in lib.maxsim_amd_last_error()
+
+
+def test_typed_backward_16bit_needs_one_entry_pass(lib):
+    # 1000 x 32 entries exceed one LDS pass of the document gradient: refused
+    # before any launch, so the caller can take the fp32 path
+    assert _typed_backward(lib, nq=1000, lq=32) == UNSUPPORTED
+    assert b"fp32" in lib.maxsim_amd_last_error()
+    # one query whose tokens alone exceed a pass (token chunks): refused too
+    assert _typed_backward(lib, nq=1, lq=40000) == UNSUPPORTED

@@ -25,6 +25,7 @@ from oracle import maxsim_oracle as oracle
 
 from ._helpers import DEVICE, GRAD_TOL, SCORE_TOL, assert_close, check_argmax, np64, npi
 from .golden.c1_inputs import digest, make_c1
+from .test_gpu_contrastive import assert_rounded_from
 
 pytestmark = pytest.mark.gpu
 
@@ -179,3 +180,19 @@ def test_c5_backward_split_and_single_pass_agree(c5):
         outs.append((dq, dd))
     torch.testing.assert_close(outs[0][0], outs[1][0], rtol=1e-5, atol=1e-7)
     torch.testing.assert_close(outs[0][1], outs[1][1], rtol=1e-5, atol=1e-7)
+
+
+def test_c5_backward_in_input_dtype_equals_cast_fp32(c5):
+    """The training step's backward writes bf16 gradients directly; at full
+    size they equal the fp32 operator's gradients cast by torch: dq bit for
+    bit, dd up to the fp32 bucket-order noise (CE's dscore has both signs, so
+    some row sums cancel to far below their terms)."""
+    q, d, off, _, scores, argmax = c5
+    nq = q.shape[0]
+    g = ((torch.softmax(scores, 1) - torch.eye(nq, device=DEVICE)) / nq).contiguous()
+    dq32, dd32 = ops.maxsim_contrastive_backward(g, q, d, off, argmax)
+    dq, dd = ops.maxsim_contrastive_backward_typed(g, q, d, off, argmax)
+    assert dq.dtype == torch.bfloat16 and dd.dtype == torch.bfloat16
+    assert torch.equal(dq, dq32.to(torch.bfloat16))
+    _, mag = ops.maxsim_contrastive_backward(g.abs(), q.abs(), d, off, argmax)
+    assert_rounded_from(dd, dd32, mag)

@@ -181,3 +181,101 @@ def test_contrastive_train_end_to_end(dtype):
     tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
     assert_close(q.grad, dq_ref, **tol)
     assert_close(d.grad, dd_ref, **tol)
+
+
+def assert_rounded_from(typed: torch.Tensor, ref32: torch.Tensor, mag: torch.Tensor) -> None:
+    """`typed` (16-bit) is `ref32` rounded to nearest, up to the fp32
+    summation-order noise of a gradient whose terms have absolute sum `mag`:
+    most elements are bit-identical to the cast, and every element is within
+    1.5 units of the 16-bit format of ref32 plus 2^-16 * mag (far above the
+    fp32 reordering error of the bucket sums, far below any real mistake)."""
+    dtype = typed.dtype
+    cast = ref32.to(dtype)
+    same = (typed.view(torch.int16) == cast.view(torch.int16)) | ((typed == 0) & (cast == 0))
+    assert float(same.float().mean()) > 0.99
+    rel = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    atol = 0.0 if dtype == torch.bfloat16 else 2.0 ** -24  # fp16 subnormal spacing
+    err = (typed.float() - ref32).abs()
+    bound = rel * ref32.abs() + 2.0 ** -16 * mag + atol
+    assert bool(torch.all(err <= bound)), float((err - bound).max())
+
+
+TYPED = [
+    pytest.param(3, 16, 64, [37, 64, 200, 17, 81], id="Nb5-gather"),
+    pytest.param(4, 32, 128, [40, 1, 300, 33, 90, 64, 7, 129, 2], id="Nb9-split"),
+    pytest.param(2, 7, 20, [9, 33, 5, 1, 2, 70, 3, 8], id="dim20-element-wise"),
+    pytest.param(600, 32, 128, [64, 10, 200, 33, 1, 128, 90, 47, 300, 5], id="Nq600-fp32-fallback"),
+    pytest.param(1, 20000, 8, [3, 17, 1, 40, 9, 2, 5, 11], id="Lq20000-fp32-fallback"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+@pytest.mark.parametrize("Nq,Lq,dim,d_lens", TYPED)
+def test_contrastive_backward_typed_equals_cast_fp32(Nq, Lq, dim, d_lens, dtype):
+    """The autograd path's operator writes the gradients in the input dtype;
+    they must be the fp32 operator's gradients cast by torch (round to
+    nearest even).  dq is summed in a fixed order, so it is bit-identical;
+    dd's bucket order can differ between runs, which changes fp32 last bits
+    (by far more than a last bit, relative to the sum, where terms of both
+    signs cancel)."""
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=Nq * 7 + dim)
+    gen = torch.Generator().manual_seed(21)
+    dscore = torch.randn(Nq, len(d_lens), generator=gen).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq32, dd32 = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    dq, dd = ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+    assert dq.dtype == dtype and dd.dtype == dtype
+    assert dq.shape == dq32.shape and dd.shape == dd32.shape
+    assert torch.equal(dq, dq32.to(dtype))
+    # absolute term sums of dd: the same routing with |dscore| and |q|
+    _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
+    assert_rounded_from(dd, dd32, mag)
+
+
+def test_contrastive_backward_typed_fp32_inputs_are_fp32():
+    q, d, off = make_contrastive(2, 16, 32, [16, 40], torch.float32, seed=5)
+    dscore = torch.randn(2, 2, generator=torch.Generator().manual_seed(2)).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq, dd = ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+    dq32, dd32 = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    assert dq.dtype == torch.float32 and torch.equal(dq, dq32)
+    torch.testing.assert_close(dd, dd32, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_contrastive_backward_zeroes_rows_outside_the_documents(grad_dtype):
+    """With offsets that start after row 0 and end before the last row, the
+    rows outside every document get a zero gradient (the reference zero-fills
+    its gradient buffers), and the rows inside match the oracle.  Called
+    through the C ABI into NaN-filled buffers, so an unwritten row shows."""
+    import ctypes
+    from pathlib import Path
+
+    dtype = torch.bfloat16
+    q, d_in, off_in = make_contrastive(3, 16, 64, [20, 33, 9], dtype, seed=13)
+    pad_head, pad_tail = 5, 7
+    d = torch.cat([torch.full((pad_head, 64), 3.0, dtype=dtype, device=DEVICE), d_in,
+                   torch.full((pad_tail, 64), -2.0, dtype=dtype, device=DEVICE)])
+    off = off_in + pad_head
+    nq, lq, dim = q.shape
+    nb, n = off.numel() - 1, d.shape[0]
+    dscore = torch.randn(nq, nb, generator=torch.Generator().manual_seed(4)).to(DEVICE)
+    _, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    dq = torch.full((nq, lq, dim), float("nan"), dtype=grad_dtype, device=DEVICE)
+    dd = torch.full((n, dim), float("nan"), dtype=grad_dtype, device=DEVICE)
+    lib = ctypes.CDLL(str(Path(maxsim_amd.__file__).resolve().parent / "libmaxsim_amd.so"))
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    fn = lib.maxsim_amd_contrastive_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P,
+                   ctypes.c_size_t, P]
+    BF16, F32 = 2, 0
+    rc = fn(BF16, F32 if grad_dtype == torch.float32 else BF16, dscore.data_ptr(), q.data_ptr(),
+            nq, lq, d.data_ptr(), n, off.data_ptr(), nb, argmax.data_ptr(), dim, dq.data_ptr(),
+            dd.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.all(dd[:pad_head] == 0) and torch.all(dd[n - pad_tail:] == 0)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d_in), npi(off_in),
+                                                 npi(argmax))
+    assert_close(dd[pad_head:n - pad_tail].float(), dd_ref, rtol=1e-2, atol=1e-3)
+    assert_close(dq.float(), dq_ref, rtol=1e-2, atol=1e-3)
