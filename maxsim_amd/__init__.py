@@ -96,14 +96,21 @@ def _require_one_device(**tensors: torch.Tensor) -> None:
 
 
 def _to_host(*tensors: torch.Tensor) -> list[np.ndarray]:
-    """One device->host copy for several small int tensors."""
-    flat = [t.detach().reshape(-1).to(torch.int64) for t in tensors]
-    sizes = [f.numel() for f in flat]
-    joined = torch.cat(flat).cpu().numpy() if flat else np.zeros(0, np.int64)
+    """One device->host copy for several small int tensors, as int64 arrays.
+
+    Tensors of one dtype are joined on the device in their own dtype (no
+    join for a single tensor) and widened on the host, so a single int32
+    offsets tensor costs one copy and no device kernel."""
+    if not tensors:
+        return []
+    flat = [t.detach().reshape(-1) for t in tensors]
+    if len({f.dtype for f in flat}) > 1:
+        flat = [f.to(torch.int64) for f in flat]
+    joined = (flat[0] if len(flat) == 1 else torch.cat(flat)).cpu().numpy().astype(np.int64)
     out, pos = [], 0
-    for n in sizes:
-        out.append(joined[pos:pos + n])
-        pos += n
+    for f in flat:
+        out.append(joined[pos:pos + f.numel()])
+        pos += f.numel()
     return out
 
 

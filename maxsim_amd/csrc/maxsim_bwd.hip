@@ -280,62 +280,94 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 // gfx950 dispatches workgroup w to XCD w % 8, and each XCD has its own L2.
 // Range r = w % kXcds of the documents is therefore gathered only by the
 // workgroups of one XCD, so each XCD's L2 serves 1/8 of D instead of all of
-// it.  A thread owns (query row, 8-element slice, range) and walks the
-// range's documents U at a time (U winning rows in flight per lane), writing
-// its fp32 partial sum to ws[range]; dq_reduce_kernel adds the kXcds parts in
-// range order, so dq is bitwise reproducible.  U = 4 measured best at C5
-// (1: 229 us, 4: 200 us, 8: 271 us, 16: 387 us: larger U costs occupancy).
+// it.  A thread owns (query row, 8-element slice, range) and writes its fp32
+// partial sum to ws[range]; dq_reduce_kernel adds the kXcds parts in range
+// order, so dq is bitwise reproducible.
+//
+// The workgroup's rows and a chunk of the range's documents form a table of
+// (source row, weight) pairs, built in LDS by one coalesced pass over the
+// argmax, offsets and dscore; the gather loop then reads only the table and
+// D, U winning rows in flight per lane, with no dependent index loads
+// between batches.  Documents are added in order, one FMA each (weight 0 for
+// an invalid entry).
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 constexpr int kDqBatch = 4;
+constexpr int kDqTable = 2048;  // (row, document) pairs staged per chunk
 
 template <typename T, int U>
 __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, bool vec, float* ws,
                                                        int rows_per_group) {
   using S = typename T::storage;
+  __shared__ int32_t t_src[kDqTable];  // [document in chunk][row in group]
+  __shared__ float t_w[kDqTable];
   const int r = blockIdx.x % kXcds;
-  const int64_t grp = blockIdx.x / kXcds;
-  const int local = threadIdx.x / a.nslices;
-  if (local >= rows_per_group) return;
-  const int64_t row = grp * rows_per_group + local;
-  if (row >= a.rows) return;
-  const int sl = threadIdx.x - local * a.nslices;
+  const int64_t row0 = (int64_t)(blockIdx.x / kXcds) * rows_per_group;
+  const int rpg = rows_per_group;
+  const int chunk = kDqTable / rpg;
+  const int tid = threadIdx.x;
+  const int local = tid / a.nslices;
+  const int64_t row = row0 + local;
+  const bool active = local < rpg && row < a.rows;
+  const int sl = tid - local * a.nslices;
   const int k0 = sl * 8;
-  const int64_t qidx = row / a.lq;
-  const int i = (int)(row - qidx * a.lq);
   const int64_t b_lo = a.nb * r / kXcds;
   const int64_t b_hi = a.nb * (r + 1) / kXcds;
   const S* __restrict__ D = static_cast<const S*>(a.d);
-  const int32_t* am = a.argmax + qidx * a.nb * a.lq + i;
-  const float* gq = a.dscore + qidx * a.nb;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int64_t b0 = b_lo; b0 < b_hi; b0 += U) {
-    int64_t src[U];
-    float wt[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t b = b0 + u;
-      src[u] = 0;
-      wt[u] = 0.0f;
-      if (b < b_hi) {
-        const int64_t s = a.doff[b], e = a.doff[b + 1];
-        const int j = am[b * a.lq];
-        if (s >= 0 && e > s && e <= a.total_d && j >= 0 && j < e - s) {
-          src[u] = s + j;
-          wt[u] = gq[b];
+  for (int64_t c0 = b_lo; c0 < b_hi; c0 += chunk) {
+    const int nc = (int)min((int64_t)chunk, b_hi - c0);
+    __syncthreads();  // the previous chunk's table is consumed
+    // consecutive threads take consecutive rows of one document: the argmax
+    // reads of a query's tokens are contiguous
+    for (int e = tid; e < nc * rpg; e += 256) {
+      const int bl = e / rpg;
+      const int lr = e - bl * rpg;
+      const int64_t rw = row0 + lr;
+      int32_t src = 0;
+      float w = 0.0f;
+      if (rw < a.rows) {
+        const int64_t qidx = rw / a.lq;
+        const int i = (int)(rw - qidx * a.lq);
+        const int64_t b = c0 + bl;
+        const int64_t s0 = a.doff[b], s1 = a.doff[b + 1];
+        const int j = a.argmax[(qidx * a.nb + b) * a.lq + i];
+        if (s0 >= 0 && s1 > s0 && s1 <= a.total_d && j >= 0 && j < s1 - s0) {
+          src = (int32_t)(s0 + j);
+          w = a.dscore[qidx * a.nb + b];
         }
       }
+      t_src[e] = src;
+      t_w[e] = w;
     }
-    // raw 16-byte fragments; widened to fp32 only inside the FMAs
-    Frag<T> v[U];
+    __syncthreads();
+    if (active) {
+      // full batches unmasked; the last one repeats its last document past
+      // the chunk end and does not add it
+      auto batch = [&](int bl, auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
+        float wt[U];
+        Frag<T> v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = load_frag<T>(D + src[u] * (int64_t)a.dim, k0, a.dim, vec);
+        for (int u = 0; u < U; ++u) {
+          const int e = (MASKED ? min(bl + u, nc - 1) : bl + u) * rpg + local;
+          wt[u] = t_w[e];
+          v[u] = load_frag<T>(D + (int64_t)t_src[e] * a.dim, k0, a.dim, vec);
+        }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int e2 = 0; e2 < 8; ++e2) acc[e2] = fmaf(wt[u], frag_elem(v[u], e2), acc[e2]);
+          for (int e2 = 0; e2 < 8; ++e2) {
+            const float t = fmaf(wt[u], frag_elem(v[u], e2), acc[e2]);
+            acc[e2] = (!MASKED || bl + u < nc) ? t : acc[e2];
+          }
+      };
+      int bl = 0;
+      for (; bl + U <= nc; bl += U) batch(bl, std::false_type{});
+      if (bl < nc) batch(bl, std::true_type{});
+    }
   }
-  store8f(ws + (int64_t)r * a.rows * a.dim + row * a.dim, k0, a.dim, vec, acc);
+  if (active) store8f(ws + (int64_t)r * a.rows * a.dim + row * a.dim, k0, a.dim, vec, acc);
 }
 
 // dq[x] = sum over the kXcds partial buffers, in range order, written in
