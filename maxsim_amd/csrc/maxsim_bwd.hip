@@ -448,6 +448,7 @@ constexpr int kDdThreads = 512;
 constexpr int kDdMaxGroup = 16;
 constexpr int kDdBatch = 8;      // bucket entries gathered per step
 constexpr int kDdBlock = 32;     // bucket entries per block sum
+constexpr int kDdSortBatch = 8;  // argmax loads in flight per thread while sorting
 
 // x / d for 0 <= x < 2^24, d >= 1, from a float reciprocal: x is exact in
 // fp32 and the rounded product is within one of the quotient (exact for
@@ -534,11 +535,31 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
         for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
         for (int x = tid; x < qc; x += kDdThreads) gst[x] = a.dscore[(q0 + x) * a.nb + b];
         __syncthreads();
+        // Entry x's target row, relative to the row pass (out of range: not
+        // in this pass or invalid).  Both sort phases read the argmax
+        // kDdSortBatch entries per thread at a time, so that many loads are in
+        // flight before the first LDS atomic waits on one.  Loads past ne read
+        // entry ne - 1 and are dropped: an unconditional load keeps the
+        // compiler from waiting on each one at a branch join.
+        auto load_targets = [&](int x0, int (&jj)[kDdSortBatch], int (&pk)[kDdSortBatch]) {
+#pragma unroll
+          for (int k = 0; k < kDdSortBatch; ++k) {
+            const int x = min(x0 + k * kDdThreads, ne - 1);
+            const int ql = div_small(x, ic, inv_ic);
+            jj[k] = am_p[ql * am_qstride + (x - ql * ic)] - r0;
+            pk[k] = x | (ql << 16);
+          }
+#pragma unroll
+          for (int k = 0; k < kDdSortBatch; ++k)
+            if (x0 + k * kDdThreads >= ne) jj[k] = -1;
+        };
         // 1. histogram of target rows
-        for (int x = tid; x < ne; x += kDdThreads) {
-          const int ql = div_small(x, ic, inv_ic);
-          const int j = am_p[ql * am_qstride + (x - ql * ic)] - r0;
-          if (j >= 0 && j < nrows) atomicAdd(&start[j + 1], 1);
+        for (int x0 = tid; x0 < ne; x0 += kDdThreads * kDdSortBatch) {
+          int jj[kDdSortBatch], pk[kDdSortBatch];
+          load_targets(x0, jj, pk);
+#pragma unroll
+          for (int k = 0; k < kDdSortBatch; ++k)
+            if (jj[k] >= 0 && jj[k] < nrows) atomicAdd(&start[jj[k] + 1], 1);
         }
         __syncthreads();
         // 2. inclusive scan of start[1..nrows] by wave 0 (lane owns a run)
@@ -564,10 +585,12 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
         for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
         __syncthreads();
         // 3. scatter packed entry ids into their row buckets
-        for (int x = tid; x < ne; x += kDdThreads) {
-          const int ql = div_small(x, ic, inv_ic);
-          const int j = am_p[ql * am_qstride + (x - ql * ic)] - r0;
-          if (j >= 0 && j < nrows) ids[atomicAdd(&cursor[j], 1)] = x | (ql << 16);
+        for (int x0 = tid; x0 < ne; x0 += kDdThreads * kDdSortBatch) {
+          int jj[kDdSortBatch], pk[kDdSortBatch];
+          load_targets(x0, jj, pk);
+#pragma unroll
+          for (int k = 0; k < kDdSortBatch; ++k)
+            if (jj[k] >= 0 && jj[k] < nrows) ids[atomicAdd(&cursor[jj[k]], 1)] = pk[k];
         }
         __syncthreads();
         // 4. per-row fp32 sums, one group of G lanes per row
