@@ -428,17 +428,20 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // (global_load_lds_dwordx4: each lane moves one 16-byte piece, a wave
   // instruction fills 1 KB of a buffer; the swizzle is applied by choosing
   // the source address of each slot).  Step k:
+  //   (0) issue the first MFMAs of tile k+1 (operands already in registers);
   //   (1) wait until this wave's loads of tile k+2 have landed, barrier --
   //       now every wave's loads of tile k+2 are in LDS and every wave has
   //       finished reading tile k's buffer (read two steps earlier);
   //   (2) issue the loads of tile k+4 into tile k's buffer;
-  //   (3) issue tile k+1's MFMAs from A fragments already in registers
-  //       into one accumulator set, and read tile k+2's fragments;
+  //   (3) issue the rest of tile k+1's MFMAs into one accumulator set, and
+  //       read tile k+2's fragments;
   //   (4) run the max/argmax epilogue of tile k from the other set -- its
-  //       VALU work and the LDS reads are interleaved with the MFMAs.
+  //       VALU work and the LDS reads are interleaved with the MFMAs;
+  //   (5) advance the load and epilogue cursors.
   // Loads have two steps to land, operand reads a whole step, and no
-  // registers are spent on global->LDS staging.  Vector-memory loads complete in issue order, so "at most N
-  // loads outstanding" (s_waitcnt vmcnt(N)) identifies completed tiles.
+  // registers are spent on global->LDS staging.  Vector-memory loads
+  // complete in issue order, so "at most N loads outstanding"
+  // (s_waitcnt vmcnt(N)) identifies completed tiles.
   int ntiles = 0;
   for (int bl = 0; bl < n_docs; ++bl) {
     int s0;
@@ -528,13 +531,28 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       }
     }
   };
-  auto mfma_tile = [&](const Frag<T> (&df)[KS], f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
+  // A tile's NBW * KS MFMAs, issued chain-interleaved (MFMA p accumulates
+  // into block p % NBW, chunk p / NBW), so consecutive MFMAs are independent.
+  // The first kPreMfma are issued before the step's wait and barrier (they
+  // only read registers): the matrix pipe then has work while the waves
+  // synchronise and issue the scalar work that follows the barrier.
+  constexpr int kPreMfma = NBW;
+  auto mfma_range = [&](auto lo_c, auto hi_c, const Frag<T> (&df)[KS],
+                        f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      acc[j] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[j][s], acc[j]);
+    for (int p = decltype(lo_c)::value; p < decltype(hi_c)::value; ++p) {
+      const int j = p % NBW;
+      const int s = p / NBW;
+      if (s == 0) acc[j] = f32x16{};
+      mma_chunk(df[s], qf[j][s], acc[j]);
     }
+  };
+  auto mfma_pre = [&](const Frag<T> (&df)[KS], f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
+    mfma_range(std::integral_constant<int, 0>{}, std::integral_constant<int, kPreMfma>{}, df, acc);
+  };
+  auto mfma_rest = [&](const Frag<T> (&df)[KS], f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
+    mfma_range(std::integral_constant<int, kPreMfma>{}, std::integral_constant<int, NBW * KS>{},
+               df, acc);
   };
 
   float m[NBW];
@@ -609,7 +627,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   f32x16 acc0[NBW], acc1[NBW];
   read_frags(std::integral_constant<int, 0>{}, fr0);
   read_frags(std::integral_constant<int, 1>{}, fr1);
-  mfma_tile(fr0, acc0);
+  mfma_pre(fr0, acc0);
+  mfma_rest(fr0, acc0);
 
   // Step k (U = k % 4): fragments of tile k+1 are in registers, tile k's
   // MFMA results in the other accumulator set.
@@ -620,22 +639,23 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     f32x16 (&acc_nxt)[NBW] = (U % 2 == 0) ? acc1 : acc0;
     Frag<T> (&fr_nxt)[KS] = (U % 2 == 0) ? fr1 : fr0;   // tile k+1
     Frag<T> (&fr_new)[KS] = (U % 2 == 0) ? fr0 : fr1;   // <- tile k+2
+    mfma_pre(fr_nxt, acc_nxt);
     // tile k+2 must be resident; this wave's loads of k+2 and k+3 may still be
     // outstanding (k+3 only if it exists)
     wait_vm(k + 3 < ntiles ? d_w : 0);
     barrier();
     dma_tile(u_const, fc);                               // tile k+4 -> buffer k % 4
-    fc = advance(fc);
-    // The cursor walks read document offsets from LDS; doing both before
-    // this step's fragment reads keeps their waits off those reads.
-    const TileCursor cc_next = advance(cc);
     // Past the last tile these reads and MFMAs see stale buffers; their
     // results are never used, and every wave keeps the same barrier count.
     read_frags(std::integral_constant<int, (U + 2) % kNB>{}, fr_new);
-    mfma_tile(fr_nxt, acc_nxt);
+    mfma_rest(fr_nxt, acc_nxt);
     epilogue(acc_cur, cc);
     if (k + 1 >= ntiles) return true;
-    cc = cc_next;
+    // The cursor walks (scalar code with branches, document offsets read
+    // from LDS) come after the MFMAs and the epilogue, off the path from
+    // the barrier to the matrix pipe.
+    fc = advance(fc);
+    cc = advance(cc);
     ++k;
     return false;
   };
