@@ -245,7 +245,8 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
 constexpr int kTiledWaves = 8;
 constexpr int kTiledThreads = kTiledWaves * 64;
 constexpr int kTileBuffers = 4;        // LDS tile ring
-constexpr int kMaxDocsPerGroup = 256;  // LDS offset table per workgroup
+constexpr int kMaxDocsPerGroup = 2048;  // LDS offset table per workgroup
+constexpr int kDocWork = 32;            // work of a document beyond its rows, in rows
 
 struct TiledArgs {
   const void* q;
@@ -259,7 +260,6 @@ struct TiledArgs {
   int nblk;   // blocks per query
   int qpw;    // queries per wave
   int n_qg;   // query groups
-  int dpw;    // documents per workgroup
   int n_dc;   // document chunks
   float* scores;
   int32_t* argmax;
@@ -363,10 +363,50 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       qf[j][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, true);
   }
 
-  const int64_t b_begin = (int64_t)dc * a.dpw;
-  const int64_t b_end = min(b_begin + (int64_t)a.dpw, a.nb);
+  // Document chunk dc: the documents whose work prefix W(b) = off[b] +
+  // kDocWork * b falls in [dc, dc + 1) * W / n_dc, W = total_d + kDocWork *
+  // nb (rows, plus one tile's worth per document for its last partial tile
+  // and its document-end work), so chunks hold equal work, not equal counts.
+  // The bounds are counts of documents below each threshold, one parallel
+  // pass over the offsets; counts partition [0, nb) for any offsets.
+  __shared__ int chunk_cnt[2];
+  if (threadIdx.x < 2) chunk_cnt[threadIdx.x] = 0;
+  __syncthreads();
+  {
+    const int64_t w_all = a.total_d + (int64_t)kDocWork * a.nb;
+    const int64_t w_lo = w_all * dc / a.n_dc;
+    const int64_t w_hi = w_all * (dc + 1) / a.n_dc;
+    int c_lo = 0, c_hi = 0;
+    for (int64_t bb = threadIdx.x; bb < a.nb; bb += kTiledThreads) {
+      const int64_t w = (int64_t)a.doff[bb] + (int64_t)kDocWork * bb;
+      c_lo += w < w_lo ? 1 : 0;
+      c_hi += w < w_hi ? 1 : 0;
+    }
+    if (c_lo) atomicAdd(&chunk_cnt[0], c_lo);
+    if (c_hi) atomicAdd(&chunk_cnt[1], c_hi);
+  }
+  __syncthreads();
+  const int64_t b_begin = dc == 0 ? 0 : chunk_cnt[0];
+  const int64_t b_end = dc == a.n_dc - 1 ? a.nb : chunk_cnt[1];
   float* __restrict__ scores = a.scores;
   int32_t* __restrict__ argmax_out = a.argmax;
+  // With non-decreasing offsets consecutive documents are kDocWork apart in
+  // W, so the host's chunk count keeps every chunk within the offset table.
+  // Only offsets that decrease or overrun total_d can break that; such a
+  // chunk is reported like documents with invalid offsets.
+  if (b_end - b_begin > kMaxDocsPerGroup) {
+    for (int64_t b = b_begin; b < b_end; ++b) {
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int64_t q = q_first + j / a.nblk;
+        if (j >= a.qpw * a.nblk || q >= a.nq) continue;
+        const int tok = (j % a.nblk) * kTileCols + c;
+        if (ARGMAX && argmax_out && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
+        if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
+      }
+    }
+    return;
+  }
   // The chunk's document offsets are copied to LDS once, so the tile walk
   // never issues global loads of its own: the only vector-memory loads in
   // flight are the tile loads, whose completion is tracked by count.
@@ -741,6 +781,20 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
   return check_launch("pair_kernel");
 }
 
+// Compute units of the current device (256 on MI355X), cached per device.
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
 // Blocks per wave for the tiled kernel, per (dtype width, KS): the query
 // fragments (NBW * KS * {4,8} VGPRs) must leave room for the document
 // fragments and accumulators at two waves per SIMD.
@@ -759,15 +813,18 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   a.qpw = NBW / a.nblk;
   const int64_t q_per_wg = (int64_t)a.qpw * kTiledWaves;
   a.n_qg = (int)((a.nq + q_per_wg - 1) / q_per_wg);
-  // Enough workgroups to fill 256 CUs several times over, but keep chunks of
-  // documents together so every workgroup streams a long tile sequence.
-  int64_t n_dc = (2048 + a.n_qg - 1) / a.n_qg;
-  if (n_dc > a.nb) n_dc = a.nb;
-  if (n_dc < (a.nb + kMaxDocsPerGroup - 1) / kMaxDocsPerGroup)
-    n_dc = (a.nb + kMaxDocsPerGroup - 1) / kMaxDocsPerGroup;
-  if (n_dc < 1) n_dc = 1;
-  a.dpw = (int)((a.nb + n_dc - 1) / n_dc);
-  a.n_dc = (int)((a.nb + a.dpw - 1) / a.dpw);
+  // About one workgroup per CU, each streaming one long tile sequence: its
+  // query group against a chunk of documents holding an equal share of the
+  // work (the chunks are found on the device), so every CU finishes at the
+  // same time and pays for one pipeline fill.  More chunks when needed to keep
+  // each chunk within the LDS offset table (documents are >= kDocWork apart
+  // in the work measure).
+  const int64_t w_all = a.total_d + (int64_t)kDocWork * a.nb;
+  const int64_t per_table = (int64_t)kDocWork * (kMaxDocsPerGroup - 1);
+  int64_t n_dc = (device_cus() + a.n_qg - 1) / a.n_qg;
+  n_dc = std::max<int64_t>(n_dc, (w_all + per_table - 1) / per_table);
+  n_dc = std::max<int64_t>(1, std::min<int64_t>(n_dc, a.nb));
+  a.n_dc = (int)n_dc;
   const int64_t total = (int64_t)a.n_qg * a.n_dc;
   const int64_t per_xcd = (total + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8));

@@ -279,3 +279,34 @@ def test_contrastive_backward_zeroes_rows_outside_the_documents(grad_dtype):
                                                  npi(argmax))
     assert_close(dd[pad_head:n - pad_tail].float(), dd_ref, rtol=1e-2, atol=1e-3)
     assert_close(dq.float(), dq_ref, rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("nb,lo,hi", [(5000, 1, 24), (2, 300, 700), (40, 1, 3000)],
+                         ids=["5000-small-docs", "2-docs", "40-docs-skewed"])
+def test_contrastive_work_balanced_chunks(nb, lo, hi):
+    """The tiled forward splits the documents into chunks of equal work (rows
+    plus a per-document share), found on the device: many small documents
+    (more chunks than one per CU, to respect the offset table), fewer
+    documents than chunks (empty chunks), and skewed lengths."""
+    gen = torch.Generator().manual_seed(nb)
+    lens = torch.randint(lo, hi + 1, (nb,), generator=gen).tolist()
+    q, d, off = make_contrastive(3, 32, 128, lens, torch.bfloat16, seed=nb + 1, unit=True)
+    scores, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    _check_forward(q, d, off, scores, argmax)
+
+
+def test_contrastive_malformed_offsets_at_the_operator_level():
+    """Offsets that decrease (the Python layer rejects them; the operator is
+    called directly): documents with an invalid range get a NaN score and
+    argmax 0, the valid ones their MaxSim, and nothing is read out of range."""
+    q, d, _ = make_contrastive(2, 32, 64, [20, 20], torch.bfloat16, seed=17)
+    off = torch.tensor([0, 10, 5, 20], dtype=torch.int32, device=DEVICE)
+    scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    assert torch.isnan(scores[:, 1]).all()
+    assert torch.all(argmax[:, 1] == 0)
+    qn, dn = np64(q), np64(d)
+    for b, (s0, e0) in [(0, (0, 10)), (2, (5, 20))]:
+        s_ref, a_ref = oracle.contrastive_forward(qn, dn[s0:e0], np.array([0, e0 - s0], dtype=np.int64))
+        assert_close(scores[:, b:b + 1], s_ref, **SCORE_TOL[torch.bfloat16])
+        check_argmax(npi(argmax[:, b:b + 1]), a_ref, lambda idx: qn[idx[0], idx[2]],
+                     lambda idx, j, s0=s0: dn[s0 + j])
