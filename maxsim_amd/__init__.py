@@ -282,8 +282,11 @@ def _check_contrastive(queries, documents, document_offsets) -> None:
         )
     _require_one_device(queries=queries, documents=documents,
                         document_offsets=document_offsets)
-    (offs,) = _to_host(document_offsets)
-    total = documents.shape[0]
+
+
+def _check_offsets(offs: np.ndarray, total: int) -> None:
+    """The host-side offset checks of the contrastive surface (reference
+    __init__.py:880-905): CSR convention, total length, strictly increasing."""
     if offs[0] != 0:
         raise ValueError(
             f"document_offsets[0] must equal 0 (CSR offset convention); got {int(offs[0])}"
@@ -460,6 +463,30 @@ def score_candidates_padded_train(queries, documents, query_lengths,
 # ---------------------------------------------------------------------------
 # Contrastive (all pairs)
 # ---------------------------------------------------------------------------
+def _checked_contrastive(queries, documents, document_offsets, launch):
+    """Validate a contrastive call and return ``launch()``.
+
+    The offsets travel to pinned host memory by an asynchronous copy queued
+    ahead of the kernels, and ``launch()`` queues the kernels before the host
+    waits for that copy, so the GPU is never idle while the host checks them.
+    Invalid offsets raise the same errors as before; the kernels already
+    queued are safe with any offsets (documents with an invalid range give
+    NaN, nothing is read out of range) and their results are dropped."""
+    _check_contrastive(queries, documents, document_offsets)
+    flat = document_offsets.detach().reshape(-1)
+    if not flat.is_cuda:  # host tensors: check first (the operators reject them anyway)
+        _check_offsets(flat.numpy().astype(np.int64), documents.shape[0])
+        return launch()
+    host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
+    host.copy_(flat, non_blocking=True)
+    copied = torch.cuda.Event()
+    copied.record()
+    result = launch()
+    copied.synchronize()
+    _check_offsets(host.numpy().astype(np.int64), documents.shape[0])
+    return result
+
+
 def score_contrastive(queries, documents, document_offsets) -> torch.Tensor:
     """Score every query against every packed document.
 
@@ -470,19 +497,20 @@ def score_contrastive(queries, documents, document_offsets) -> torch.Tensor:
     Returns:
         ``[Nq, Nb]`` fp32 scores.
     """
-    _check_contrastive(queries, documents, document_offsets)
-    return ops.maxsim_contrastive_forward(
-        queries.contiguous(), documents.contiguous(),
-        document_offsets.to(torch.int32).contiguous())
+    return _checked_contrastive(
+        queries, documents, document_offsets,
+        lambda: ops.maxsim_contrastive_forward(queries.contiguous(), documents.contiguous(),
+                                               document_offsets.to(torch.int32).contiguous()))
 
 
 def score_contrastive_with_argmax(queries, documents,
                                   document_offsets) -> Tuple[torch.Tensor, torch.Tensor]:
     """As :func:`score_contrastive`, plus int32 argmax ``[Nq, Nb, Lq]``."""
-    _check_contrastive(queries, documents, document_offsets)
-    return ops.maxsim_contrastive_forward_with_argmax(
-        queries.contiguous(), documents.contiguous(),
-        document_offsets.to(torch.int32).contiguous())
+    return _checked_contrastive(
+        queries, documents, document_offsets,
+        lambda: ops.maxsim_contrastive_forward_with_argmax(
+            queries.contiguous(), documents.contiguous(),
+            document_offsets.to(torch.int32).contiguous()))
 
 
 class _ContrastiveFn(torch.autograd.Function):
@@ -508,5 +536,6 @@ class _ContrastiveFn(torch.autograd.Function):
 
 def score_contrastive_train(queries, documents, document_offsets) -> torch.Tensor:
     """Differentiable :func:`score_contrastive` (gradients accumulated in fp32)."""
-    _check_contrastive(queries, documents, document_offsets)
-    return _ContrastiveFn.apply(queries, documents, document_offsets)
+    return _checked_contrastive(
+        queries, documents, document_offsets,
+        lambda: _ContrastiveFn.apply(queries, documents, document_offsets))

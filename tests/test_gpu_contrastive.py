@@ -310,3 +310,28 @@ def test_contrastive_malformed_offsets_at_the_operator_level():
         assert_close(scores[:, b:b + 1], s_ref, **SCORE_TOL[torch.bfloat16])
         check_argmax(npi(argmax[:, b:b + 1]), a_ref, lambda idx: qn[idx[0], idx[2]],
                      lambda idx, j, s0=s0: dn[s0 + j])
+
+
+CONTRASTIVE_FNS = [maxsim_amd.score_contrastive, maxsim_amd.score_contrastive_with_argmax,
+                   maxsim_amd.score_contrastive_train]
+
+
+@pytest.mark.parametrize("fn", CONTRASTIVE_FNS, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("bad,pattern", [
+    ([1, 33, 65, 97, 129], "0|start|offset"),
+    ([0, 32, 16, 96, 128], "monoton|decreas|order|offset"),
+    ([0, 25, 50, 75, 100], "total|match|offset"),
+    ([0, 0, 64, 96, 128], "strictly|empty|offset"),
+    ([-5, 32, 64, 96, 140], "0|start|offset"),
+])
+def test_contrastive_bad_device_offsets_raise_after_queueing(fn, bad, pattern):
+    """Device offsets are checked on the host while the kernels already run
+    (the check waits only for their copy): bad offsets still raise the
+    reference's ValueError, the queued kernels are safe with them, and the
+    device is in a good state afterwards."""
+    q, d, _ = make_contrastive(2, 16, 32, [32, 32, 32, 32], torch.float16, seed=3)
+    with pytest.raises(ValueError, match=pattern):
+        fn(q, d, torch.tensor(bad, dtype=torch.int32, device=DEVICE))
+    torch.cuda.synchronize()
+    good = torch.tensor([0, 32, 64, 96, 128], dtype=torch.int32, device=DEVICE)
+    _check_forward(q, d, good, maxsim_amd.score_contrastive(q, d, good), None)
