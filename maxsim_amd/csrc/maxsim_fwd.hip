@@ -144,10 +144,25 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
   int64_t loaded_q = -1;
   int loaded_lq = -1, loaded_g = -1;
 
+  // The run is pipelined across pairs: the next pair's rows are resolved
+  // while the current one is scored, and its first tile is loaded in place
+  // of a prefetch at the current pair's last tile, so a pair starts with its
+  // first tile already in flight (queries that change still load here).
+  auto load_tile = [&](const Pair& q_pr, int t, Frag<T> (&f)[KS]) __attribute__((always_inline)) {
+    const int r = min(t * kTileRows + c, q_pr.ld - 1);
+    const S* row = D + (q_pr.d_row0 + r) * (int64_t)dim;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) f[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
+  };
+  Pair pr = resolve_pair(a, p_begin);
+  Frag<T> df[KS];
+  bool df_ready = false;  // df holds tile 0 of pr
   for (int64_t p = p_begin; p < p_end; ++p) {
-    const Pair pr = resolve_pair(a, p);
+    const Pair nx = (p + 1 < p_end) ? resolve_pair(a, p + 1) : Pair{0, 0, 0, 0, false};
     if (!pr.ok) {
       write_invalid_pair(a, p, lane);
+      pr = nx;
+      df_ready = false;
       continue;
     }
     const int nblk = (pr.lq + kTileCols - 1) / kTileCols;
@@ -174,23 +189,17 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
         m[qb] = -__builtin_inff();
         am[qb] = 0;
       }
-      Frag<T> df[KS];
-      {
-        const int r = min(c, pr.ld - 1);
-        const S* row = D + (pr.d_row0 + r) * (int64_t)dim;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-          df[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
-      }
+      if (!df_ready) load_tile(pr, 0, df);
+      df_ready = false;
+      // after the last tile of the last pass comes the next pair's tile 0
+      const bool hand_over = (g0 + QB >= nblk) && nx.ok;
       for (int t = 0; t < ntiles; ++t) {
         Frag<T> nf[KS];
-        if (t + 1 < ntiles) {
-          const int r = min((t + 1) * kTileRows + c, pr.ld - 1);
-          const S* row = D + (pr.d_row0 + r) * (int64_t)dim;
-#pragma unroll
-          for (int s = 0; s < KS; ++s)
-            nf[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, vec);
-        }
+        const bool more = t + 1 < ntiles;
+        if (more)
+          load_tile(pr, t + 1, nf);
+        else if (hand_over)
+          load_tile(nx, 0, nf);
         // rows past the document end were loaded as copies of its last row
         // and cannot win (see tile_update), so no masking is needed
         f32x16 acc[QB];
@@ -203,11 +212,12 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
           tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
-        if (t + 1 < ntiles) {
+        if (more || hand_over) {
 #pragma unroll
           for (int s = 0; s < KS; ++s) df[s] = nf[s];
         }
       }
+      df_ready = hand_over;
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const int blk = g0 + qb;
@@ -226,6 +236,7 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
         a.argmax[p * a.slots + t] = 0;
     }
     if (lane == kHalfSumLane) a.scores[p] = score;
+    pr = nx;
   }
 }
 
