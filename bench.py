@@ -1,6 +1,6 @@
 """Benchmark of the MaxSim hot path on one MI355X.
 
-Headline workload (the north-star configuration):
+Headline workload (configuration C5, the largest contrastive batch):
 one contrastive training step -- score_contrastive_train over Nq=Nb=512
 queries/documents (Lq=32, Ld ~ U[128, 1024], dim=128, bf16, L2-normalised
 Gaussian embeddings, 1% duplicated document tokens), cross-entropy over the
@@ -8,7 +8,7 @@ diagonal, backward to dQ and dD.  Inputs are resident in HBM before timing.
 
 Printed as ONE JSON line.  ``value`` is the step throughput in TFLOP/s
 (F = 2*D*Nq*Lq*T_d forward flops per step / step time); ``ms_per_step`` is the
-user-level step time (including the API's host-side offset validation).
+user-level step time (including the API's offset validation).
 Kernel-level timings, the other configurations (C2 contrastive 64x64, C3
 padded rerank docs/s, C4 packed pairs) and the CPU baseline are extra fields.
 
@@ -171,7 +171,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the contrastive batch would shard); run with --gpus 1",
+              "(the contrastive batch would shard by query rows); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 

@@ -1,4 +1,4 @@
-"""Seeded generator of BASELINE config C1 (padded rerank, fp32): 8 queries x 16
+"""Seeded generator of configuration C1 (padded rerank, fp32): 8 queries x 16
 candidates, Lq = 32, documents padded to Ld = 300 with real lengths uniform in
 [64, 300], dim = 128, L2-normalised Gaussian rows.  Pad rows hold garbage on
 purpose (they must be ignored).  Shared by make_golden.py and the tests."""

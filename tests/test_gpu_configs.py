@@ -1,4 +1,4 @@
-"""The five BASELINE configurations on the GPU, at their real sizes.
+"""The five benchmark configurations (C1-C5) on the GPU, at their real sizes.
 
 C1 against the committed golden fixture; C2 and C4 against the oracle in
 full; C3 on a slice of queries (any slice of the chunk-seeded set is
