@@ -205,6 +205,43 @@ def _packed_layout(queries, query_offsets, documents, document_offsets,
     return max_q
 
 
+def _checked_packed(queries, query_offsets, documents, document_offsets,
+                    pair_query_ids, pair_document_ids, max_q_len, launch):
+    """Validate a packed call and return ``launch(max_q_len)``.
+
+    Without ``max_q_len`` the output shape depends on the offsets, so they are
+    read and checked before anything is launched.  With it, the offsets and
+    ids travel to pinned host memory by asynchronous copies queued ahead of
+    the kernels, ``launch`` queues the kernels, and only then does the host
+    wait for the copies and run the same checks with the same errors.  The
+    packed kernels are safe with any offsets and ids (an invalid pair gives a
+    NaN score, nothing is read out of range), so work queued before a failing
+    check is harmless and its result is dropped."""
+    if max_q_len is None or not query_offsets.is_cuda:
+        return launch(_resolve_max_q_len(max_q_len, _packed_layout(
+            queries, query_offsets, documents, document_offsets,
+            pair_query_ids, pair_document_ids)))
+    if max_q_len <= 0:
+        raise ValueError(f"max_q_len must be > 0; got {max_q_len}")
+    hosts = []
+    for t in (query_offsets, document_offsets, pair_query_ids, pair_document_ids):
+        flat = t.detach().reshape(-1)
+        host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
+        host.copy_(flat, non_blocking=True)
+        hosts.append(host)
+    copied = torch.cuda.Event()
+    copied.record()
+    result = launch(int(max_q_len))
+    copied.synchronize()
+    qoff, doff, qids, dids = (h.numpy().astype(np.int64) for h in hosts)
+    max_q = _check_csr(qoff, queries.shape[0], "query_offsets")
+    _check_csr(doff, documents.shape[0], "document_offsets")
+    _check_ids(qids, qoff.size - 1, "pair_query_ids")
+    _check_ids(dids, doff.size - 1, "pair_document_ids")
+    _resolve_max_q_len(max_q_len, max_q)
+    return result
+
+
 def _resolve_max_q_len(max_q_len, actual: int) -> int:
     if max_q_len is None:
         return actual
@@ -327,13 +364,13 @@ def score_pairs_packed(queries, query_offsets, documents, document_offsets,
     """
     _check_packed_common(queries, query_offsets, documents, document_offsets,
                          pair_query_ids, pair_document_ids, argmax_wording=False)
-    mql = _resolve_max_q_len(max_q_len, _packed_layout(
-        queries, query_offsets, documents, document_offsets,
-        pair_query_ids, pair_document_ids))
-    return ops.maxsim_forward(
-        queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
-        document_offsets.contiguous(), pair_query_ids.contiguous(),
-        pair_document_ids.contiguous(), mql)
+    return _checked_packed(
+        queries, query_offsets, documents, document_offsets, pair_query_ids,
+        pair_document_ids, max_q_len,
+        lambda mql: ops.maxsim_forward(
+            queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
+            document_offsets.contiguous(), pair_query_ids.contiguous(),
+            pair_document_ids.contiguous(), mql))
 
 
 def score_pairs_packed_with_argmax(queries, query_offsets, documents, document_offsets,
@@ -343,13 +380,13 @@ def score_pairs_packed_with_argmax(queries, query_offsets, documents, document_o
     query token: int32 ``[num_pairs, max_q_len]`` (0 beyond a pair's length)."""
     _check_packed_common(queries, query_offsets, documents, document_offsets,
                          pair_query_ids, pair_document_ids, argmax_wording=True)
-    mql = _resolve_max_q_len(max_q_len, _packed_layout(
-        queries, query_offsets, documents, document_offsets,
-        pair_query_ids, pair_document_ids))
-    return ops.maxsim_packed_forward_with_argmax(
-        queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
-        document_offsets.contiguous(), pair_query_ids.contiguous(),
-        pair_document_ids.contiguous(), mql)
+    return _checked_packed(
+        queries, query_offsets, documents, document_offsets, pair_query_ids,
+        pair_document_ids, max_q_len,
+        lambda mql: ops.maxsim_packed_forward_with_argmax(
+            queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
+            document_offsets.contiguous(), pair_query_ids.contiguous(),
+            pair_document_ids.contiguous(), mql))
 
 
 class _PackedFn(torch.autograd.Function):
@@ -382,11 +419,11 @@ def score_pairs_packed_train(queries, query_offsets, documents, document_offsets
     """Differentiable :func:`score_pairs_packed` (fp32 gradients)."""
     _check_packed_common(queries, query_offsets, documents, document_offsets,
                          pair_query_ids, pair_document_ids, argmax_wording=True)
-    mql = _resolve_max_q_len(max_q_len, _packed_layout(
-        queries, query_offsets, documents, document_offsets,
-        pair_query_ids, pair_document_ids))
-    return _PackedFn.apply(queries, query_offsets, documents, document_offsets,
-                           pair_query_ids, pair_document_ids, mql)
+    return _checked_packed(
+        queries, query_offsets, documents, document_offsets, pair_query_ids,
+        pair_document_ids, max_q_len,
+        lambda mql: _PackedFn.apply(queries, query_offsets, documents, document_offsets,
+                                    pair_query_ids, pair_document_ids, mql))
 
 
 # ---------------------------------------------------------------------------

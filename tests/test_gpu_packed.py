@@ -165,3 +165,40 @@ def test_packed_train_end_to_end(dtype):
     tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
     assert_close(q.grad, dq_ref, **tol)
     assert_close(d.grad, dd_ref, **tol)
+
+
+PACKED_FNS = [maxsim_amd.score_pairs_packed, maxsim_amd.score_pairs_packed_with_argmax,
+              maxsim_amd.score_pairs_packed_train]
+
+
+def _packed_dev():
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(13, 64, generator=gen).to(torch.float16).to(DEVICE)
+    d = torch.randn(20, 64, generator=gen).to(torch.float16).to(DEVICE)
+    i32 = dict(dtype=torch.int32, device=DEVICE)
+    return q, torch.tensor([0, 5, 13], **i32), d, torch.tensor([0, 20], **i32), i32
+
+
+@pytest.mark.parametrize("fn", PACKED_FNS, ids=lambda f: f.__name__)
+def test_packed_bad_device_inputs_with_max_q_len_raise_after_queueing(fn):
+    """With max_q_len given, the offsets and ids are checked on the host while
+    the kernels already run: every bad input still raises the reference's
+    error, and the queued kernels are safe with it."""
+    q, qo, d, do, i32 = _packed_dev()
+    one = torch.tensor([1], **i32)
+    zero = torch.tensor([0], **i32)
+    with pytest.raises(RuntimeError, match="0|offset|start"):
+        fn(q, torch.tensor([1, 5, 13], **i32), d, do, one, zero, max_q_len=8)
+    with pytest.raises(RuntimeError, match="total|equal|offset"):
+        fn(q, qo, d, torch.tensor([0, 30], **i32), one, zero, max_q_len=8)
+    with pytest.raises(RuntimeError, match="out of range"):
+        fn(q, qo, d, do, torch.tensor([-1], **i32), zero, max_q_len=8)
+    with pytest.raises(RuntimeError, match="out of range"):
+        fn(q, qo, d, do, one, torch.tensor([7], **i32), max_q_len=8)
+    with pytest.raises(ValueError, match="max_q_len"):
+        fn(q, qo, d, do, one, zero, max_q_len=5)   # query 1 has 8 tokens
+    torch.cuda.synchronize()
+    # the device is fine and a good call gives the oracle's answer
+    s = maxsim_amd.score_pairs_packed(q, qo, d, do, one, zero, max_q_len=8)
+    s_ref, _ = oracle.packed_forward(np64(q), npi(qo), np64(d), npi(do), npi(one), npi(zero), 8)
+    assert_close(s, s_ref, **SCORE_TOL[torch.float16])
