@@ -383,7 +383,13 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   __shared__ int chunk_cnt[2];
   if (threadIdx.x < 2) chunk_cnt[threadIdx.x] = 0;
   __syncthreads();
-  {
+  if (a.n_dc >= a.nb) {
+    // one document per chunk: nothing to balance
+    if (threadIdx.x == 0) {
+      chunk_cnt[0] = dc;
+      chunk_cnt[1] = (int)min((int64_t)dc + 1, a.nb);
+    }
+  } else {
     const int64_t w_all = a.total_d + (int64_t)kDocWork * a.nb;
     const int64_t w_lo = w_all * dc / a.n_dc;
     const int64_t w_hi = w_all * (dc + 1) / a.n_dc;

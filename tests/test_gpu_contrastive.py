@@ -335,3 +335,17 @@ def test_contrastive_bad_device_offsets_raise_after_queueing(fn, bad, pattern):
     torch.cuda.synchronize()
     good = torch.tensor([0, 32, 64, 96, 128], dtype=torch.int32, device=DEVICE)
     _check_forward(q, d, good, maxsim_amd.score_contrastive(q, d, good), None)
+
+
+def test_contrastive_decreasing_offsets_overflowing_a_chunk():
+    """3000 documents whose offsets decrease so that the work measure puts all
+    of them in one chunk, more than the 2048-entry offset table holds: the
+    chunk is reported like invalid documents (NaN score, argmax 0), with no
+    out-of-range access.  (Every document here has end < start anyway.)"""
+    nb = 3000
+    q, d, _ = make_contrastive(2, 32, 128, [4096], torch.bfloat16, seed=23)
+    off = (100000 - 32 * torch.arange(nb + 1, dtype=torch.int64)).to(torch.int32).to(DEVICE)
+    scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    torch.cuda.synchronize()
+    assert torch.isnan(scores).all()
+    assert torch.all(argmax == 0)
