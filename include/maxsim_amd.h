@@ -20,7 +20,8 @@
  *   ids        : int32.
  *   argmax     : int32, one slot per (pair, query token); slots beyond a
  *                pair's real query length are written as 0.
- *   grads      : fp32, shaped like the embeddings they belong to; every
+ *   grads      : fp32 (the *_typed entry points can write the input dtype
+ *                instead), shaped like the embeddings they belong to; every
  *                element is written (callers need not zero them).
  *
  * Semantics shared by all forward entry points (reference maxsim.cu:412-443,
@@ -112,6 +113,27 @@ int maxsim_amd_packed_backward(
     const int32_t* pair_query_ids, const int32_t* pair_document_ids,
     int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
     float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* maxsim_amd_packed_backward with the gradients written in `grad_dtype`:
+ * MAXSIM_FLOAT32, or the input dtype, in which case each element is the
+ * fp32 sum rounded to nearest even, as casting the fp32 gradients would
+ * give (up to the fp32 summation order, which varies between runs for the
+ * document gradient).  No counterpart in the reference: its autograd
+ * Function (torch-ext/maxsim/__init__.py:445-454) returns fp32 gradients
+ * and autograd casts them to the input dtype in a separate pass; writing the
+ * input dtype directly removes that pass and halves the gradient writes.  A
+ * 16-bit grad_dtype needs the grouped path (the workspace and
+ * max_q_len < 65536) when num_pairs > 0; without it the call returns
+ * MAXSIM_ERR_UNSUPPORTED before launching anything. */
+int maxsim_amd_packed_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream);
 
 /* ---- Padded rerank ------------------------------------------------------ */

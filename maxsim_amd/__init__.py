@@ -14,7 +14,9 @@ Every function validates its inputs on the host with the reference's error
 types and messages, then calls an operator of :mod:`maxsim_amd._ops`, which
 runs hand-written HIP kernels (fused MFMA forward with an in-register
 max/argmax epilogue; argmax-driven gather/scatter backward).  Scores are fp32;
-gradients are fp32 (autograd casts them to the input dtype for ``.grad``).
+gradients are summed in fp32.  ``.grad`` has the input dtype: the padded
+Function returns fp32 gradients that autograd casts, the contrastive and
+packed Functions have the kernels write that rounding (nearest even) directly.
 
 The pure-PyTorch ``*_reference`` functions of the reference package are
 exported too (:mod:`maxsim_amd.reference`) for benchmarks and comparisons;
@@ -121,7 +123,8 @@ def _check_lengths(values: np.ndarray, max_len: int, name: str) -> None:
         raise ValueError(f"{name} values must be <= padded length {max_len}")
 
 
-def _check_padded(queries, documents, query_lengths, doc_lengths):
+def _check_padded_meta(queries, documents, query_lengths, doc_lengths):
+    """Shapes, dtypes and devices of a padded call (no device data read)."""
     if queries.dim() != 3:
         raise ValueError(f"queries must be 3-D [B, Lq, D]; got shape {tuple(queries.shape)}")
     if documents.dim() != 4:
@@ -153,10 +156,40 @@ def _check_padded(queries, documents, query_lengths, doc_lengths):
     _require_index("doc_lengths", doc_lengths)
     _require_one_device(queries=queries, documents=documents,
                         query_lengths=query_lengths, doc_lengths=doc_lengths)
-    qlen, dlen = _to_host(query_lengths, doc_lengths)
+    return B, C, Lq, Ld, D
+
+
+def _checked_padded(queries, documents, query_lengths, doc_lengths, launch):
+    """Validate a padded call and return ``launch(B, C, Lq, Ld)``.
+
+    The lengths travel to pinned host memory by asynchronous copies queued
+    ahead of the kernels, ``launch`` queues the kernels, and only then does
+    the host wait for the copies and check the values, with the same errors
+    as a check made before the launch.  The padded kernels are safe with any
+    lengths (a candidate with a length outside ``(0, Ld]`` or a query length
+    outside ``(0, Lq]`` gives a NaN score, nothing is read out of range), so
+    work queued before a failing check is harmless and its result is
+    dropped."""
+    B, C, Lq, Ld, _ = _check_padded_meta(queries, documents, query_lengths, doc_lengths)
+    if not query_lengths.is_cuda:  # host tensors: check first (the operators reject them anyway)
+        qlen, dlen = _to_host(query_lengths, doc_lengths)
+        _check_lengths(qlen, Lq, "query_lengths")
+        _check_lengths(dlen, Ld, "doc_lengths")
+        return launch(B, C, Lq, Ld)
+    hosts = []
+    for t in (query_lengths, doc_lengths):
+        flat = t.detach().reshape(-1)
+        host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
+        host.copy_(flat, non_blocking=True)
+        hosts.append(host)
+    copied = torch.cuda.Event()
+    copied.record()
+    result = launch(B, C, Lq, Ld)
+    copied.synchronize()
+    qlen, dlen = (h.numpy().astype(np.int64) for h in hosts)
     _check_lengths(qlen, Lq, "query_lengths")
     _check_lengths(dlen, Ld, "doc_lengths")
-    return B, C, Lq, Ld, D
+    return result
 
 
 def _check_pair_ids(pair_query_ids, pair_document_ids) -> None:
@@ -407,7 +440,10 @@ class _PackedFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dscore):
         q, qoff, d, doff, qids, dids, argmax = ctx.saved_tensors
-        dq, dd = ops.maxsim_packed_backward(
+        # gradients in the inputs' dtype, written by the kernels (the fp32
+        # sums rounded to nearest even: what autograd's cast of the reference's
+        # fp32 gradients gives, without the separate cast pass)
+        dq, dd = ops.maxsim_packed_backward_typed(
             dscore.contiguous().to(torch.float32), q, qoff, d, doff, qids, dids,
             argmax, ctx.max_q_len)
         return dq, None, dd, None, None, None, None
@@ -416,7 +452,7 @@ class _PackedFn(torch.autograd.Function):
 def score_pairs_packed_train(queries, query_offsets, documents, document_offsets,
                              pair_query_ids, pair_document_ids, *,
                              max_q_len=None) -> torch.Tensor:
-    """Differentiable :func:`score_pairs_packed` (fp32 gradients)."""
+    """Differentiable :func:`score_pairs_packed` (gradients accumulated in fp32)."""
     _check_packed_common(queries, query_offsets, documents, document_offsets,
                          pair_query_ids, pair_document_ids, argmax_wording=True)
     return _checked_packed(
@@ -451,19 +487,23 @@ def score_candidates_padded(queries, documents, query_lengths, doc_lengths) -> t
     Returns:
         ``[B, C]`` fp32 scores.
     """
-    B, C, Lq, Ld, _ = _check_padded(queries, documents, query_lengths, doc_lengths)
-    q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
-    return ops.maxsim_padded_forward(q, ql, d, dl, int(Lq), int(Ld), int(C)).view(B, C)
+    def launch(B, C, Lq, Ld):
+        q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
+        return ops.maxsim_padded_forward(q, ql, d, dl, int(Lq), int(Ld), int(C)).view(B, C)
+
+    return _checked_padded(queries, documents, query_lengths, doc_lengths, launch)
 
 
 def score_candidates_padded_with_argmax(queries, documents, query_lengths,
                                         doc_lengths) -> Tuple[torch.Tensor, torch.Tensor]:
     """As :func:`score_candidates_padded`, plus int32 argmax ``[B, C, Lq]``
     (first index wins ties; 0 beyond ``query_lengths[b]``)."""
-    B, C, Lq, Ld, _ = _check_padded(queries, documents, query_lengths, doc_lengths)
-    q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
-    s, a = ops.maxsim_padded_forward_with_argmax(q, ql, d, dl, int(Lq), int(Ld), int(C))
-    return s.view(B, C), a.view(B, C, Lq)
+    def launch(B, C, Lq, Ld):
+        q, d, ql, dl = _padded_flat(queries, documents, query_lengths, doc_lengths)
+        s, a = ops.maxsim_padded_forward_with_argmax(q, ql, d, dl, int(Lq), int(Ld), int(C))
+        return s.view(B, C), a.view(B, C, Lq)
+
+    return _checked_padded(queries, documents, query_lengths, doc_lengths, launch)
 
 
 class _PaddedFn(torch.autograd.Function):
@@ -492,9 +532,10 @@ class _PaddedFn(torch.autograd.Function):
 
 def score_candidates_padded_train(queries, documents, query_lengths,
                                   doc_lengths) -> torch.Tensor:
-    """Differentiable :func:`score_candidates_padded` (fp32 gradients)."""
-    _check_padded(queries, documents, query_lengths, doc_lengths)
-    return _PaddedFn.apply(queries, documents, query_lengths, doc_lengths)
+    """Differentiable :func:`score_candidates_padded` (gradients accumulated in fp32)."""
+    return _checked_padded(
+        queries, documents, query_lengths, doc_lengths,
+        lambda *_: _PaddedFn.apply(queries, documents, query_lengths, doc_lengths))
 
 
 # ---------------------------------------------------------------------------

@@ -3,10 +3,11 @@
 ``ops`` is ``torch.ops.maxsim_amd``: the nine operators of the reference's
 torch extension (torch-ext/torch_binding.cpp:7-90) with identical names,
 argument order and return arity, implemented by hand-written HIP kernels for
-gfx950 behind the C ABI in ``include/maxsim_amd.h``.  One more operator,
-``maxsim_contrastive_backward_typed``, is the contrastive backward with the
-gradients in the inputs' dtype; the autograd Function uses it so that torch
-does not cast fp32 gradients in a separate pass.
+gfx950 behind the C ABI in ``include/maxsim_amd.h``.  Two more operators,
+``maxsim_contrastive_backward_typed`` and ``maxsim_packed_backward_typed``,
+are the contrastive and packed backwards with the gradients in the inputs'
+dtype; the autograd Functions use them so that torch does not cast fp32
+gradients in a separate pass.
 
 Importing this module loads ``_maxsim_amd_torch.so`` (which pulls in
 ``libmaxsim_amd.so``).  There is no fallback: if the native build is missing
@@ -100,6 +101,12 @@ def _(queries, documents, document_offsets):
 @torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward")
 def _(dscore, queries, documents, document_offsets, argmax):
     return _f32(queries, queries.shape), _f32(documents, documents.shape)
+
+
+@torch.library.register_fake("maxsim_amd::maxsim_packed_backward_typed")
+def _(dscore, queries, query_offsets, documents, document_offsets,
+      pair_query_ids, pair_document_ids, argmax, max_q_len):
+    return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
 
 
 @torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward_typed")

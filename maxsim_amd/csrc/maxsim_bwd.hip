@@ -739,8 +739,8 @@ struct PackedBwdArgs {
   const int32_t* qids;
   const int32_t* dids;
   const int32_t* argmax;
-  float* dq;
-  float* dd;
+  void* dq;  // fp32, or the 16-bit output type of the grouped kernels
+  void* dd;
   int64_t nq;
   int64_t nd;
   int64_t total_q;
@@ -781,8 +781,8 @@ __global__ __launch_bounds__(256) void packed_bwd_kernel(PackedBwdArgs a,
       float qv[8], dv[8];
       load8f<T>(Q + (qs + i) * (int64_t)a.dim, sl * 8, a.dim, vec, qv);
       load8f<T>(D + (ds + j) * (int64_t)a.dim, sl * 8, a.dim, vec, dv);
-      float* dqr = a.dq + (qs + i) * (int64_t)a.dim + sl * 8;
-      float* ddr = a.dd + (ds + j) * (int64_t)a.dim + sl * 8;
+      float* dqr = static_cast<float*>(a.dq) + (qs + i) * (int64_t)a.dim + sl * 8;
+      float* ddr = static_cast<float*>(a.dd) + (ds + j) * (int64_t)a.dim + sl * 8;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (sl * 8 + u < a.dim) {
@@ -895,22 +895,23 @@ __global__ __launch_bounds__(256) void pair_scatter_kernel(PackedBwdArgs a, Pack
 constexpr int kGroupThreads = 256;
 constexpr int kPairStage = 256;  // pairs staged in LDS at a time
 
-// Zero the rows [0, off[0]) and [off[nseg], total) of a [total, dim] fp32
-// output: the rows before the first and after the last segment, which no
-// per-segment workgroup owns.
-__global__ __launch_bounds__(256) void zero_outside_kernel(float* out, const int32_t* off,
+// Zero the rows [0, off[0]) and [off[nseg], total) of a [total, dim] output
+// of element type E (float or a 16-bit type): the rows before the first and
+// after the last segment, which no per-segment workgroup owns.
+template <typename E>
+__global__ __launch_bounds__(256) void zero_outside_kernel(E* out, const int32_t* off,
                                                            int64_t nseg, int64_t total, int dim) {
   const int64_t head = min(max((int64_t)off[0], (int64_t)0), total);
   const int64_t tail = min(max((int64_t)off[nseg], head), total);
   const int64_t n_head = head * dim, n_tail = (total - tail) * dim;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n_head + n_tail; x += stride)
-    out[x < n_head ? x : tail * dim + (x - n_head)] = 0.0f;
+    out[x < n_head ? x : tail * dim + (x - n_head)] = E(0);
 }
 
 // dq: workgroup = (query qi, block of its tokens); thread = (token row,
 // 8-element slice).
-template <typename T, bool VEC>
+template <typename T, bool VEC, typename O>
 __global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs a,
                                                                   PackedGroups g) {
   using S = typename T::storage;
@@ -976,7 +977,7 @@ __global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs 
           }
       }
     }
-    if (active && i < lq) store8f(a.dq + (qs + i) * (int64_t)a.dim, k0, a.dim, VEC, acc);
+    if (active && i < lq) store8<O>(out_at<O>(a.dq, (qs + i) * (int64_t)a.dim), k0, a.dim, VEC, acc);
   }
 }
 
@@ -988,10 +989,20 @@ __global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs 
 // write the row once, zeros for rows no entry points at.  Entries are taken
 // in stages of nc pairs x tc tokens (nc * tc <= kPkEntries), documents longer
 // than kPkRows rows in row passes; later stages add to the rows written.
+// With a 16-bit output type O, documents that need more than one stage are
+// left to dd_packed_multi_kernel (a 16-bit row cannot hold the partial sum a
+// later stage would add to), so every row written here is written once.
 constexpr int kPkRows = 2048;     // rows bucketed per pass
 constexpr int kPkEntries = 4096;  // entries per stage (bucket ids held in LDS)
 
-template <typename T, bool VEC, int NS>
+// True when a document with n_pairs pairs needs more than one stage of
+// entries in dd_packed_kernel.
+__device__ __forceinline__ bool dd_packed_multi_stage(const PackedBwdArgs& a, int n_pairs) {
+  const int tc = min(a.slots, kPkEntries);
+  return a.slots > tc || n_pairs > min(kPairStage, kPkEntries / tc);
+}
+
+template <typename T, bool VEC, int NS, typename O>
 __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs a,
                                                                   PackedGroups g, int G) {
   using S = typename T::storage;
@@ -1010,6 +1021,9 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
   const int grp = tid / G, gl = tid - grp * G;
   const int ngroups = kGroupThreads / G;
   const int k_lo = g.dstart[di], k_hi = g.dstart[di + 1];
+  if constexpr (O::bytes != 4) {
+    if (dd_packed_multi_stage(a, k_hi - k_lo)) return;
+  }
   const int dim = a.dim;
   const int tc = min(a.slots, kPkEntries);               // tokens per stage
   const int stage_pairs = min(kPairStage, kPkEntries / tc);
@@ -1082,12 +1096,12 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
         // 4. per-row fp32 sums, one group of G lanes per row
         for (int rr = grp; rr < nrows; rr += ngroups) {
           float acc[NS][8];
-          float* dst = a.dd + (ds + r0 + rr) * (int64_t)dim;
+          void* dst = out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim);
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int sl = gl + u * G;
-            if (sl < sl_hi && !first) {
-              load8f<F32>(dst, sl * 8, dim, VEC, acc[u]);
+            if (O::bytes == 4 && sl < sl_hi && !first) {  // never taken for 16-bit O
+              load8f<F32>(static_cast<const float*>(dst), sl * 8, dim, VEC, acc[u]);
             } else {
 #pragma unroll
               for (int x = 0; x < 8; ++x) acc[u][x] = 0.0f;
@@ -1139,12 +1153,93 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int sl = gl + u * G;
-            if (sl < sl_hi) store8f(dst, sl * 8, dim, VEC, acc[u]);
+            if (sl < sl_hi) store8<O>(dst, sl * 8, dim, VEC, acc[u]);
           }
         }
       }
       c0 += nc;
     } while (c0 < k_hi);
+  }
+}
+
+// dd with a 16-bit output type O for the documents dd_packed_kernel leaves
+// (those needing more than one stage of entries); workgroups stride over the
+// documents and skip the others.  Rows are taken
+// kPkAccFloats / dim at a time with their fp32 sums in LDS; a wave adds one
+// entry g_k * q_row at a time (lanes over the embedding dimension, LDS
+// atomics), over every stage of the document's pairs, then each row is
+// rounded to O and written once.  The order of the LDS additions varies, so
+// these rows can differ between runs in the last bits.
+constexpr int kPkAccFloats = 16384;  // 64 KiB of row sums
+
+template <typename T, typename O>
+__global__ __launch_bounds__(kGroupThreads) void dd_packed_multi_kernel(PackedBwdArgs a,
+                                                                        PackedGroups g) {
+  using S = typename T::storage;
+  __shared__ float acc[kPkAccFloats];
+  __shared__ int64_t st_qs[kPairStage];
+  __shared__ int32_t st_lq[kPairStage];
+  __shared__ int32_t st_p[kPairStage];
+  __shared__ float st_g[kPairStage];
+  const int dim = a.dim;
+  const int slots = a.slots;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kWaves = kGroupThreads / 64;
+  const int rows_per_pass = kPkAccFloats / dim;  // >= 64 for dim <= 256
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  uint16_t* __restrict__ out = static_cast<uint16_t*>(a.dd);
+  // di, and so every branch on it, is uniform over the workgroup
+  for (int64_t di = blockIdx.x; di < a.nd; di += gridDim.x) {
+    const int64_t ds = a.doff[di], de = a.doff[di + 1];
+    if (ds < 0 || de <= ds || de > a.total_d) continue;
+    const int k_lo = g.dstart[di], k_hi = g.dstart[di + 1];
+    if (!dd_packed_multi_stage(a, k_hi - k_lo)) continue;
+    const int ld = (int)(de - ds);
+    for (int r0 = 0; r0 < ld; r0 += rows_per_pass) {
+      const int nrows = min(rows_per_pass, ld - r0);
+      const int n_el = nrows * dim;
+      __syncthreads();  // the previous pass has read its sums
+      for (int x = tid; x < n_el; x += kGroupThreads) acc[x] = 0.0f;
+      for (int c0 = k_lo; c0 < k_hi; c0 += kPairStage) {
+        const int nc = min(kPairStage, k_hi - c0);
+        __syncthreads();  // sums zeroed; the previous stage's pairs are no longer read
+        if (tid < nc) {
+          const int p = g.dlist[c0 + tid];
+          const int64_t qi = a.qids[p];
+          const int64_t qs = a.qoff[qi];
+          st_qs[tid] = qs;
+          st_lq[tid] = (int)(a.qoff[qi + 1] - qs);
+          st_p[tid] = p;
+          st_g[tid] = a.dscore[p];
+        }
+        __syncthreads();
+        // entry e = (pair k, token i); one wave per entry, uniform branches
+        const int64_t ne = (int64_t)nc * slots;
+        for (int64_t e = wave; e < ne; e += kWaves) {
+          const int k = (int)(e / slots);
+          const int i = (int)(e - (int64_t)k * slots);
+          if (i >= st_lq[k]) continue;
+          const int jt = a.argmax[(int64_t)st_p[k] * slots + i];
+          if (jt < r0 || jt >= r0 + nrows) continue;
+          const int j = jt - r0;
+          const S* qrow = Q + (st_qs[k] + i) * (int64_t)dim;
+          const float gk = st_g[k];
+          for (int x = lane; x < dim; x += 64) {
+            float v;
+            if constexpr (__is_same(T, BF16))
+              v = __uint_as_float((uint32_t)qrow[x] << 16);
+            else if constexpr (__is_same(T, F16))
+              v = (float)__builtin_bit_cast(_Float16, qrow[x]);
+            else
+              v = qrow[x];
+            atomicAdd(&acc[j * dim + x], gk * v);
+          }
+        }
+      }
+      __syncthreads();
+      uint16_t* dst = out + (ds + r0) * (int64_t)dim;
+      for (int x = tid; x < n_el; x += kGroupThreads) dst[x] = to_out16<O>(acc[x]);
+    }
   }
 }
 
@@ -1255,31 +1350,61 @@ static void launch_dd_padded(const PaddedDdArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(dd_padded_kernel<T>, grid, dim3(256), 0, st, a);
 }
 
-template <typename T>
-static void launch_packed_grouped(const PackedBwdArgs& a, const PackedGroups& g, bool vec,
-                                  int G, hipStream_t st) {
+// O: output type of the gradients (F32, or T for 16-bit gradients).
+template <typename T, typename O>
+static void launch_packed_grouped_o(const PackedBwdArgs& a, const PackedGroups& g, bool vec,
+                                    int G, hipStream_t st) {
   if (a.nq > 0) {
     const int rows_per_pass = kGroupThreads / a.nslices;
     const dim3 grid((unsigned)a.nq, (unsigned)((a.slots + rows_per_pass - 1) / rows_per_pass));
     if (vec)
-      hipLaunchKernelGGL((dq_packed_kernel<T, true>), grid, dim3(kGroupThreads), 0, st, a, g);
+      hipLaunchKernelGGL((dq_packed_kernel<T, true, O>), grid, dim3(kGroupThreads), 0, st, a, g);
     else
-      hipLaunchKernelGGL((dq_packed_kernel<T, false>), grid, dim3(kGroupThreads), 0, st, a, g);
+      hipLaunchKernelGGL((dq_packed_kernel<T, false, O>), grid, dim3(kGroupThreads), 0, st, a, g);
   }
   if (a.nd > 0) {
     const bool two = a.nslices > G;
     const dim3 grid((unsigned)a.nd);
     if (vec && two)
-      hipLaunchKernelGGL((dd_packed_kernel<T, true, 2>), grid, dim3(kGroupThreads), 0, st, a, g, G);
+      hipLaunchKernelGGL((dd_packed_kernel<T, true, 2, O>), grid, dim3(kGroupThreads), 0, st, a,
+                         g, G);
     else if (vec)
-      hipLaunchKernelGGL((dd_packed_kernel<T, true, 1>), grid, dim3(kGroupThreads), 0, st, a, g, G);
+      hipLaunchKernelGGL((dd_packed_kernel<T, true, 1, O>), grid, dim3(kGroupThreads), 0, st, a,
+                         g, G);
     else if (two)
-      hipLaunchKernelGGL((dd_packed_kernel<T, false, 2>), grid, dim3(kGroupThreads), 0, st, a, g,
-                         G);
+      hipLaunchKernelGGL((dd_packed_kernel<T, false, 2, O>), grid, dim3(kGroupThreads), 0, st, a,
+                         g, G);
     else
-      hipLaunchKernelGGL((dd_packed_kernel<T, false, 1>), grid, dim3(kGroupThreads), 0, st, a, g,
-                         G);
+      hipLaunchKernelGGL((dd_packed_kernel<T, false, 1, O>), grid, dim3(kGroupThreads), 0, st, a,
+                         g, G);
+    if constexpr (O::bytes != 4) {
+      const dim3 grid_m((unsigned)std::min<int64_t>(a.nd, 1024));
+      hipLaunchKernelGGL((dd_packed_multi_kernel<T, O>), grid_m, dim3(kGroupThreads), 0, st, a,
+                         g);
+    }
   }
+}
+
+template <typename T>
+static void launch_packed_grouped(const PackedBwdArgs& a, const PackedGroups& g, bool vec,
+                                  int G, bool out16, hipStream_t st) {
+  if constexpr (T::bytes == 2) {
+    if (out16) {
+      launch_packed_grouped_o<T, T>(a, g, vec, G, st);
+      return;
+    }
+  }
+  launch_packed_grouped_o<T, F32>(a, g, vec, G, st);
+}
+
+static void launch_zero_outside(void* out, bool out16, const int32_t* off, int64_t nseg,
+                                int64_t total, int64_t dim, hipStream_t st) {
+  if (out16)
+    hipLaunchKernelGGL(zero_outside_kernel<uint16_t>, dim3(64), dim3(256), 0, st,
+                       static_cast<uint16_t*>(out), off, nseg, total, (int)dim);
+  else
+    hipLaunchKernelGGL(zero_outside_kernel<float>, dim3(64), dim3(256), 0, st,
+                       static_cast<float*>(out), off, nseg, total, (int)dim);
 }
 
 template <typename T>
@@ -1506,17 +1631,20 @@ size_t maxsim_amd_packed_backward_workspace_size(int64_t num_queries, int64_t nu
   return (size_t)ints * sizeof(int32_t);
 }
 
-int maxsim_amd_packed_backward(
-    maxsim_dtype dtype, const float* dscore, const void* queries,
+int maxsim_amd_packed_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
     int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
     const void* documents, int64_t total_d_tokens,
     const int32_t* document_offsets, int64_t num_documents,
     const int32_t* pair_query_ids, const int32_t* pair_document_ids,
     int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
-    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream) {
   clear_error();
   if (int e = check_dtype(dtype)) return e;
+  if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
+    return fail(MAXSIM_ERR_INVALID, "grad_dtype must be FLOAT32 or the input dtype");
+  const bool out16 = grad_dtype != MAXSIM_FLOAT32;
   if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
       num_documents < 0 || num_pairs < 0)
     return fail(MAXSIM_ERR_INVALID, "negative size");
@@ -1530,9 +1658,14 @@ int maxsim_amd_packed_backward(
       maxsim_amd_packed_backward_workspace_size(num_queries, num_documents, num_pairs);
   const bool grouped = num_pairs > 0 && workspace && workspace_bytes >= ws_need &&
                        max_q_len < (1 << 16) && num_pairs < INT32_MAX;
+  // 16-bit gradients are written once per row, which only the grouped
+  // kernels do (the atomic path adds into fp32 rows)
+  if (out16 && num_pairs > 0 && !grouped)
+    return fail(MAXSIM_ERR_UNSUPPORTED,
+                "16-bit gradients need the workspace and max_q_len < 65536; use fp32 gradients");
   if (!grouped) {
-    if (total_q_tokens > 0) launch_fill(dqueries, total_q_tokens * dim, st);
-    if (total_d_tokens > 0) launch_fill(ddocuments, total_d_tokens * dim, st);
+    if (total_q_tokens > 0) launch_fill_grad(dqueries, total_q_tokens * dim, out16, st);
+    if (total_d_tokens > 0) launch_fill_grad(ddocuments, total_d_tokens * dim, out16, st);
     if (int e = check_launch("fill_zero_kernel")) return e;
   }
   if (num_pairs == 0) return MAXSIM_OK;
@@ -1586,15 +1719,30 @@ int maxsim_amd_packed_backward(
   hipLaunchKernelGGL(pair_scatter_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
   if (int e = check_launch("pair grouping kernels")) return e;
   if (total_q_tokens > 0)
-    hipLaunchKernelGGL(zero_outside_kernel, dim3(64), dim3(256), 0, st, dqueries, query_offsets,
-                       num_queries, total_q_tokens, (int)dim);
+    launch_zero_outside(dqueries, out16, query_offsets, num_queries, total_q_tokens, dim, st);
   if (total_d_tokens > 0)
-    hipLaunchKernelGGL(zero_outside_kernel, dim3(64), dim3(256), 0, st, ddocuments,
-                       document_offsets, num_documents, total_d_tokens, (int)dim);
+    launch_zero_outside(ddocuments, out16, document_offsets, num_documents, total_d_tokens, dim,
+                        st);
   const int G = pow2_at_least(nslices < 16 ? nslices : 16);  // lanes per dd row
   const bool vec_g = vec && aligned16b(dqueries) && aligned16b(ddocuments);
-  MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, st);
+  MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, out16, st);
   return check_launch("dq_packed_kernel / dd_packed_kernel");
+}
+
+int maxsim_amd_packed_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    float* dqueries, float* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  return maxsim_amd_packed_backward_typed(
+      dtype, MAXSIM_FLOAT32, dscore, queries, total_q_tokens, query_offsets, num_queries,
+      documents, total_d_tokens, document_offsets, num_documents, pair_query_ids,
+      pair_document_ids, num_pairs, argmax, max_q_len, dim, dqueries, ddocuments, workspace,
+      workspace_bytes, stream);
 }
 
 }  // extern "C"

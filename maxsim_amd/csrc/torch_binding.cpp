@@ -178,10 +178,13 @@ std::tuple<Tensor, Tensor> maxsim_packed_forward_with_argmax(
   return {scores, argmax};
 }
 
-std::tuple<Tensor, Tensor> maxsim_packed_backward(
+// grads_in_input_dtype: gradients in the inputs' dtype (the typed entry
+// point rounds each fp32 sum to nearest even, like a cast); where that path is
+// unsupported, compute in fp32 and cast.
+std::tuple<Tensor, Tensor> packed_backward_impl(
     Tensor dscore, Tensor queries, Tensor query_offsets, Tensor documents,
     Tensor document_offsets, Tensor pair_query_ids, Tensor pair_document_ids,
-    Tensor argmax, int64_t max_q_len) {
+    Tensor argmax, int64_t max_q_len, bool grads_in_input_dtype) {
   TORCH_CHECK(max_q_len > 0, "max_q_len must be > 0");
   Packed p = prep_packed(queries, query_offsets, documents, document_offsets,
                          pair_query_ids, pair_document_ids, max_q_len);
@@ -194,8 +197,6 @@ std::tuple<Tensor, Tensor> maxsim_packed_backward(
   TORCH_CHECK(argmax.numel() == np * p.mql, "argmax must be [num_pairs, max_q_len]");
   Tensor g = dscore.contiguous();
   Tensor am = argmax.contiguous();
-  Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, f32_opts(p.q));
-  Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, f32_opts(p.q));
   c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
   // workspace for grouping the pairs by query and document on the device
   // (see maxsim_amd_packed_backward_workspace_size)
@@ -203,14 +204,47 @@ std::tuple<Tensor, Tensor> maxsim_packed_backward(
       maxsim_amd_packed_backward_workspace_size(p.qoff.numel() - 1, p.doff.numel() - 1, np);
   Tensor ws = at::empty({(int64_t)((ws_bytes + 3) / 4)},
                         p.q.options().dtype(at::kInt));
-  check_status(maxsim_amd_packed_backward(
-      to_dtype(p.q), g.data_ptr<float>(), p.q.data_ptr(), p.q.size(0),
-      p.qoff.data_ptr<int32_t>(), p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0),
-      p.doff.data_ptr<int32_t>(), p.doff.numel() - 1, p.qids.data_ptr<int32_t>(),
-      p.dids.data_ptr<int32_t>(), np, am.data_ptr<int32_t>(), p.mql, p.q.size(1),
-      dq.data_ptr<float>(), dd.data_ptr<float>(), ws.data_ptr(), ws_bytes,
-      current_stream(p.q)));
+  const maxsim_dtype dt = to_dtype(p.q);
+  auto run = [&](maxsim_dtype grad_dt, const at::TensorOptions& opts) {
+    Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, opts);
+    Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, opts);
+    const int rc = maxsim_amd_packed_backward_typed(
+        dt, grad_dt, g.data_ptr<float>(), p.q.data_ptr(), p.q.size(0),
+        p.qoff.data_ptr<int32_t>(), p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0),
+        p.doff.data_ptr<int32_t>(), p.doff.numel() - 1, p.qids.data_ptr<int32_t>(),
+        p.dids.data_ptr<int32_t>(), np, am.data_ptr<int32_t>(), p.mql, p.q.size(1),
+        dq.data_ptr(), dd.data_ptr(), ws.data_ptr(), ws_bytes, current_stream(p.q));
+    return std::make_tuple(rc, dq, dd);
+  };
+  if (grads_in_input_dtype && dt != MAXSIM_FLOAT32) {
+    auto [rc, dq, dd] = run(dt, p.q.options());
+    if (rc == MAXSIM_OK) return {dq, dd};
+    // ERR_UNSUPPORTED is returned before any launch; fall through to fp32
+    TORCH_CHECK(rc == MAXSIM_ERR_UNSUPPORTED, "maxsim_amd: ", maxsim_amd_last_error());
+  }
+  auto [rc, dq, dd] = run(MAXSIM_FLOAT32, f32_opts(p.q));
+  check_status(rc);
+  if (grads_in_input_dtype && dt != MAXSIM_FLOAT32)
+    return {dq.to(p.q.scalar_type()), dd.to(p.q.scalar_type())};
   return {dq, dd};
+}
+
+std::tuple<Tensor, Tensor> maxsim_packed_backward(
+    Tensor dscore, Tensor queries, Tensor query_offsets, Tensor documents,
+    Tensor document_offsets, Tensor pair_query_ids, Tensor pair_document_ids,
+    Tensor argmax, int64_t max_q_len) {
+  return packed_backward_impl(dscore, queries, query_offsets, documents, document_offsets,
+                              pair_query_ids, pair_document_ids, argmax, max_q_len, false);
+}
+
+// Not one of the reference's operators: the autograd Function's backward,
+// with gradients in the inputs' dtype.
+std::tuple<Tensor, Tensor> maxsim_packed_backward_typed(
+    Tensor dscore, Tensor queries, Tensor query_offsets, Tensor documents,
+    Tensor document_offsets, Tensor pair_query_ids, Tensor pair_document_ids,
+    Tensor argmax, int64_t max_q_len) {
+  return packed_backward_impl(dscore, queries, query_offsets, documents, document_offsets,
+                              pair_query_ids, pair_document_ids, argmax, max_q_len, true);
 }
 
 // ---- padded ---------------------------------------------------------------
@@ -448,6 +482,9 @@ TORCH_LIBRARY(maxsim_amd, m) {
   m.def("maxsim_contrastive_backward(Tensor dscore, Tensor queries, Tensor documents, "
         "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
   // not in the reference: gradients in the inputs' dtype (used by autograd)
+  m.def("maxsim_packed_backward_typed(Tensor dscore, Tensor queries, Tensor query_offsets, "
+        "Tensor documents, Tensor document_offsets, Tensor pair_query_ids, "
+        "Tensor pair_document_ids, Tensor argmax, int max_q_len) -> (Tensor, Tensor)");
   m.def("maxsim_contrastive_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
         "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
 }
@@ -459,6 +496,7 @@ TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
   m.impl("maxsim_padded_backward", &maxsim_padded_backward);
   m.impl("maxsim_packed_forward_with_argmax", &maxsim_packed_forward_with_argmax);
   m.impl("maxsim_packed_backward", &maxsim_packed_backward);
+  m.impl("maxsim_packed_backward_typed", &maxsim_packed_backward_typed);
   m.impl("maxsim_contrastive_forward", &maxsim_contrastive_forward);
   m.impl("maxsim_contrastive_forward_with_argmax",
          &maxsim_contrastive_forward_with_argmax);

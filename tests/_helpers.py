@@ -112,3 +112,20 @@ def check_argmax(kernel_am: np.ndarray, oracle_am: np.ndarray, qvec, dvec,
             f"argmax mismatch at {idx}: kernel {jk}, oracle {jo}, similarity gap {gap}"
         )
     assert bad.shape[0] <= max(4, kernel_am.size // 1000), f"{bad.shape[0]} argmax mismatches"
+
+
+def assert_rounded_from(typed: torch.Tensor, ref32: torch.Tensor, mag: torch.Tensor) -> None:
+    """`typed` (16-bit) is `ref32` rounded to nearest, up to the fp32
+    summation-order noise of a gradient whose terms have absolute sum `mag`:
+    most elements are bit-identical to the cast, and every element is within
+    1.5 units of the 16-bit format of ref32 plus 2^-16 * mag (far above the
+    fp32 reordering error of the bucket sums, far below any real mistake)."""
+    dtype = typed.dtype
+    cast = ref32.to(dtype)
+    same = (typed.view(torch.int16) == cast.view(torch.int16)) | ((typed == 0) & (cast == 0))
+    assert float(same.float().mean()) > 0.99
+    rel = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    atol = 0.0 if dtype == torch.bfloat16 else 2.0 ** -24  # fp16 subnormal spacing
+    err = (typed.float() - ref32).abs()
+    bound = rel * ref32.abs() + 2.0 ** -16 * mag + atol
+    assert bool(torch.all(err <= bound)), float((err - bound).max())

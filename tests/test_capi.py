@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 14, names
+    assert len(names) == 15, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 4
+    assert lib.maxsim_amd_abi_version() == 5
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -159,3 +159,26 @@ def test_typed_backward_16bit_needs_one_entry_pass(lib):
     assert b"fp32" in lib.maxsim_amd_last_error()
     # one query whose tokens alone exceed a pass (token chunks): refused too
     assert _typed_backward(lib, nq=1, lq=40000) == UNSUPPORTED
+
+
+def _typed_packed_backward(lib, dtype=BF16, grad_dtype=BF16, npairs=3, mql=8, ws=None, ws_bytes=0):
+    fn = lib.maxsim_amd_packed_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, P, I64, P, I64, P, I64, P, P, I64, P,
+                   I64, I64, P, P, P, ctypes.c_size_t, P]
+    one = P(16)
+    return fn(dtype, grad_dtype, one, one, 10, one, 2, one, 20, one, 3, one, one, npairs, one, mql,
+              64, one, one, ws, ws_bytes, None)
+
+
+def test_typed_packed_backward_rejects_a_third_grad_dtype(lib):
+    assert _typed_packed_backward(lib, dtype=BF16, grad_dtype=F16) == INVALID
+    assert b"grad_dtype" in lib.maxsim_amd_last_error()
+
+
+def test_typed_packed_backward_16bit_needs_the_grouped_path(lib):
+    # without the workspace the gradients would be fp32 atomics: refused
+    # before any launch, so the caller can take the fp32 path
+    assert _typed_packed_backward(lib) == UNSUPPORTED
+    assert b"fp32" in lib.maxsim_amd_last_error()
+    # max_q_len beyond the 16-bit entry ids of the grouped kernels: refused too
+    assert _typed_packed_backward(lib, mql=70000, ws=P(16), ws_bytes=1 << 20) == UNSUPPORTED

@@ -11,8 +11,8 @@ import maxsim_amd
 from maxsim_amd._ops import ops
 from oracle import maxsim_oracle as oracle
 
-from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, check_argmax,
-                       make_contrastive, np64, npi)
+from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, assert_rounded_from,
+                       check_argmax, make_contrastive, np64, npi)
 
 pytestmark = pytest.mark.gpu
 
@@ -181,23 +181,6 @@ def test_contrastive_train_end_to_end(dtype):
     tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
     assert_close(q.grad, dq_ref, **tol)
     assert_close(d.grad, dd_ref, **tol)
-
-
-def assert_rounded_from(typed: torch.Tensor, ref32: torch.Tensor, mag: torch.Tensor) -> None:
-    """`typed` (16-bit) is `ref32` rounded to nearest, up to the fp32
-    summation-order noise of a gradient whose terms have absolute sum `mag`:
-    most elements are bit-identical to the cast, and every element is within
-    1.5 units of the 16-bit format of ref32 plus 2^-16 * mag (far above the
-    fp32 reordering error of the bucket sums, far below any real mistake)."""
-    dtype = typed.dtype
-    cast = ref32.to(dtype)
-    same = (typed.view(torch.int16) == cast.view(torch.int16)) | ((typed == 0) & (cast == 0))
-    assert float(same.float().mean()) > 0.99
-    rel = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
-    atol = 0.0 if dtype == torch.bfloat16 else 2.0 ** -24  # fp16 subnormal spacing
-    err = (typed.float() - ref32).abs()
-    bound = rel * ref32.abs() + 2.0 ** -16 * mag + atol
-    assert bool(torch.all(err <= bound)), float((err - bound).max())
 
 
 TYPED = [

@@ -12,8 +12,8 @@ import maxsim_amd
 from maxsim_amd._ops import ops
 from oracle import maxsim_oracle as oracle
 
-from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, check_argmax,
-                       make_packed, np64, npi)
+from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, assert_rounded_from,
+                       check_argmax, make_packed, np64, npi, offsets_from_lengths)
 
 pytestmark = pytest.mark.gpu
 
@@ -202,3 +202,114 @@ def test_packed_bad_device_inputs_with_max_q_len_raise_after_queueing(fn):
     s = maxsim_amd.score_pairs_packed(q, qo, d, do, one, zero, max_q_len=8)
     s_ref, _ = oracle.packed_forward(np64(q), npi(qo), np64(d), npi(do), npi(one), npi(zero), 8)
     assert_close(s, s_ref, **SCORE_TOL[torch.float16])
+
+
+def _typed_vs_fp32(q, qoff, d, doff, qids, dids, seed):
+    """Typed packed backward against the fp32 operator cast to the input
+    dtype (round to nearest even), up to fp32 summation-order noise; both
+    gradients are also checked against the oracle."""
+    dtype = q.dtype
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    mql = am.shape[1]
+    g = torch.randn(qids.numel(), generator=torch.Generator().manual_seed(seed)).to(DEVICE)
+    dq32, dd32 = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, mql)
+    dq, dd = ops.maxsim_packed_backward_typed(g, q, qoff, d, doff, qids, dids, am, mql)
+    assert dq.dtype == dtype and dd.dtype == dtype
+    assert dq.shape == dq32.shape and dd.shape == dd32.shape
+    # absolute term sums: the same routing with |g| and |d| (dq), |g| and |q| (dd)
+    mag_q, _ = ops.maxsim_packed_backward(g.abs(), q, qoff, d.abs(), doff, qids, dids, am, mql)
+    _, mag_d = ops.maxsim_packed_backward(g.abs(), q.abs(), qoff, d, doff, qids, dids, am, mql)
+    assert_rounded_from(dq, dq32, mag_q)
+    assert_rounded_from(dd, dd32, mag_d)
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), np64(q), npi(qoff), np64(d), npi(doff),
+                                            npi(qids), npi(dids), npi(am))
+    assert_close(dq, dq_ref, rtol=1e-2, atol=1e-2)
+    assert_close(dd, dd_ref, rtol=1e-2, atol=1e-2)
+
+
+TYPED = [
+    # nq, nd, npairs, dim, q range, d range, hot query / document
+    pytest.param(6, 11, 17, 64, (4, 32), (8, 200), False, id="basic"),
+    pytest.param(5, 7, 13, 20, (1, 64), (1, 64), False, id="dim20-element-wise"),
+    pytest.param(7, 13, 900, 64, (4, 40), (8, 300), True, id="hot-document-multi-stage"),
+    pytest.param(5, 6, 400, 128, (8, 64), (300, 1000), True, id="hot-long-documents-row-passes"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+@pytest.mark.parametrize("nq,nd,npairs,dim,qr,dr,hot", TYPED)
+def test_packed_backward_typed_equals_cast_fp32(nq, nd, npairs, dim, qr, dr, hot, dtype):
+    """The autograd path's operator writes the gradients in the input dtype.
+    Documents whose entries fit one LDS stage are written by the grouped dD
+    kernel; a document in hundreds of pairs takes the LDS-accumulator kernel
+    (several row passes when longer than its 128 rows at dim 128)."""
+    q, qoff, d, doff, qids, dids = make_packed(nq, nd, npairs, dim, qr, dr, dtype,
+                                               seed=npairs + dim)
+    if hot:
+        qids[: npairs // 2] = 2
+        dids[npairs // 3:] = 1
+    _typed_vs_fp32(q, qoff, d, doff, qids, dids, seed=8)
+
+
+def test_packed_backward_typed_query_longer_than_a_stage():
+    """A query of 4100 tokens (more than the 4096 entries of one LDS stage):
+    every document takes the LDS-accumulator kernel."""
+    gen = torch.Generator().manual_seed(12)
+    ql = torch.tensor([4100, 30])
+    dl = torch.tensor([50, 7, 200])
+    q = torch.randn(int(ql.sum()), 32, generator=gen).to(torch.bfloat16).to(DEVICE)
+    d = torch.randn(int(dl.sum()), 32, generator=gen).to(torch.bfloat16).to(DEVICE)
+    qoff, doff = offsets_from_lengths(ql).to(DEVICE), offsets_from_lengths(dl).to(DEVICE)
+    qids = torch.tensor([0, 1, 0, 0, 1], dtype=torch.int32, device=DEVICE)
+    dids = torch.tensor([0, 0, 2, 0, 2], dtype=torch.int32, device=DEVICE)
+    _typed_vs_fp32(q, qoff, d, doff, qids, dids, seed=9)
+
+
+def test_packed_backward_typed_zeroes_rows_outside_segments():
+    """16-bit gradients of rows before the first and after the last segment
+    are zero; document 2 is in no pair and gets zero rows."""
+    gen = torch.Generator().manual_seed(4)
+    q = torch.randn(12, 32, generator=gen).to(torch.bfloat16).to(DEVICE)
+    d = torch.randn(24, 32, generator=gen).to(torch.bfloat16).to(DEVICE)
+    qoff = torch.tensor([2, 5, 9], dtype=torch.int32, device=DEVICE)
+    doff = torch.tensor([3, 10, 16, 20], dtype=torch.int32, device=DEVICE)
+    qids = torch.tensor([0, 1, 1, 0], dtype=torch.int32, device=DEVICE)
+    dids = torch.tensor([1, 0, 1, 0], dtype=torch.int32, device=DEVICE)
+    _, am = ops.maxsim_packed_forward_with_argmax(q, qoff, d, doff, qids, dids, 4)
+    g = torch.randn(4, generator=gen).to(DEVICE)
+    dq32, dd32 = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, 4)
+    dq, dd = ops.maxsim_packed_backward_typed(g, q, qoff, d, doff, qids, dids, am, 4)
+    assert dq.dtype == torch.bfloat16 and dd.dtype == torch.bfloat16
+    assert torch.all(dq[:2] == 0) and torch.all(dq[9:] == 0)
+    assert torch.all(dd[:3] == 0) and torch.all(dd[16:] == 0)
+    torch.testing.assert_close(dq.float(), dq32.to(torch.bfloat16).float(), rtol=2 ** -7, atol=1e-6)
+    torch.testing.assert_close(dd.float(), dd32.to(torch.bfloat16).float(), rtol=2 ** -7, atol=1e-6)
+
+
+def test_packed_backward_typed_fp32_inputs_are_fp32():
+    q, qoff, d, doff, qids, dids = make_packed(4, 5, 9, 32, (2, 20), (4, 50), torch.float32, seed=3)
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    g = torch.randn(9, generator=torch.Generator().manual_seed(1)).to(DEVICE)
+    dq, dd = ops.maxsim_packed_backward_typed(g, q, qoff, d, doff, qids, dids, am, am.shape[1])
+    dq32, dd32 = ops.maxsim_packed_backward(g, q, qoff, d, doff, qids, dids, am, am.shape[1])
+    assert dq.dtype == torch.float32 and dd.dtype == torch.float32
+    torch.testing.assert_close(dq, dq32, rtol=1e-6, atol=1e-7)
+    torch.testing.assert_close(dd, dd32, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+def test_packed_train_grads_in_input_dtype(dtype):
+    """score_pairs_packed_train: .grad has the input dtype and is the fp32
+    operator's gradient rounded, as autograd's cast would give."""
+    q, qoff, d, doff, qids, dids = make_packed(5, 9, 40, 64, (4, 40), (8, 200), dtype, seed=15)
+    qg, dg = q.clone().requires_grad_(True), d.clone().requires_grad_(True)
+    w = torch.randn(40, generator=torch.Generator().manual_seed(2)).to(DEVICE)
+    (maxsim_amd.score_pairs_packed_train(qg, qoff, dg, doff, qids, dids) * w).sum().backward()
+    assert qg.grad.dtype == dtype and dg.grad.dtype == dtype
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    mql = am.shape[1]
+    dq32, dd32 = ops.maxsim_packed_backward(w, q, qoff, d, doff, qids, dids, am, mql)
+    mag_q, _ = ops.maxsim_packed_backward(w.abs(), q, qoff, d.abs(), doff, qids, dids, am, mql)
+    _, mag_d = ops.maxsim_packed_backward(w.abs(), q.abs(), qoff, d, doff, qids, dids, am, mql)
+    assert_rounded_from(qg.grad, dq32, mag_q)
+    assert_rounded_from(dg.grad, dd32, mag_d)

@@ -125,3 +125,64 @@ def test_padded_train_end_to_end(dtype):
     tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
     assert_close(q.grad, dq_ref, **tol)
     assert_close(d.grad, dd_ref, **tol)
+
+
+def test_padded_operator_invalid_lengths_give_nan_only_there():
+    """The padded kernels range-check every length they read: a candidate or
+    query whose length is outside (0, Ld] / (0, Lq] scores NaN with argmax 0,
+    every other candidate is unchanged, and nothing is read out of range."""
+    B, C, Lq, Ld, D = 3, 4, 16, 24, 32
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, D, torch.bfloat16, seed=31)
+    args = (q.reshape(B * Lq, D).contiguous(), None, d.reshape(B * C * Ld, D).contiguous())
+    s_good, a_good = ops.maxsim_padded_forward_with_argmax(
+        args[0], qlen, args[2], dlen.reshape(-1).contiguous(), Lq, Ld, C)
+    bad_q = qlen.clone()
+    bad_q[2] = Lq + 1
+    bad_d = dlen.clone()
+    bad_d[0, 1] = 0
+    bad_d[1, 3] = Ld + 5
+    bad_d[1, 0] = -7
+    s, a = ops.maxsim_padded_forward_with_argmax(
+        args[0], bad_q, args[2], bad_d.reshape(-1).contiguous(), Lq, Ld, C)
+    torch.cuda.synchronize()
+    s, a = s.view(B, C), a.view(B, C, Lq)
+    invalid = torch.zeros(B, C, dtype=torch.bool)
+    invalid[2, :] = True
+    invalid[0, 1] = invalid[1, 3] = invalid[1, 0] = True
+    invalid = invalid.to(DEVICE)
+    assert torch.isnan(s[invalid]).all()
+    assert torch.all(a[invalid] == 0)
+    assert torch.equal(s[~invalid], s_good.view(B, C)[~invalid])
+    assert torch.equal(a[~invalid], a_good.view(B, C, Lq)[~invalid])
+
+
+PADDED_FNS = [maxsim_amd.score_candidates_padded, maxsim_amd.score_candidates_padded_with_argmax,
+              maxsim_amd.score_candidates_padded_train]
+
+
+@pytest.mark.parametrize("fn", PADDED_FNS, ids=lambda f: f.__name__)
+@pytest.mark.parametrize("which,value,pattern", [
+    ("q", 0, "query_lengths must contain values > 0"),
+    ("q", 17, "query_lengths values must be <= padded length 16"),
+    ("d", 0, "doc_lengths must contain values > 0"),
+    ("d", -3, "doc_lengths must contain values > 0"),
+    ("d", 25, "doc_lengths values must be <= padded length 24"),
+])
+def test_padded_bad_device_lengths_raise_after_queueing(fn, which, value, pattern):
+    """Device lengths are checked on the host while the kernels already run
+    (the check waits only for their copy): bad lengths still raise the
+    reference's ValueError, the queued kernels are safe with them, and the
+    device is in a good state afterwards."""
+    B, C, Lq, Ld, D = 2, 3, 16, 24, 32
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, D, torch.float16, seed=37)
+    bq, bd = qlen.clone(), dlen.clone()
+    if which == "q":
+        bq[1] = value
+    else:
+        bd[1, 2] = value
+    with pytest.raises(ValueError, match=pattern):
+        fn(q, d, bq, bd)
+    torch.cuda.synchronize()
+    s_ref, _ = oracle.padded_forward(np64(q), np64(d), npi(qlen), npi(dlen))
+    assert_close(maxsim_amd.score_candidates_padded(q, d, qlen, dlen), s_ref,
+                 **SCORE_TOL[torch.float16])
