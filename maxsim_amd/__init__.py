@@ -116,6 +116,38 @@ def _to_host(*tensors: torch.Tensor) -> list[np.ndarray]:
     return out
 
 
+_COPY_STREAMS: dict = {}
+
+
+def _host_copies_async(*tensors: torch.Tensor):
+    """Queue device->host copies of small int tensors into pinned memory on a
+    side stream (default priority, one per device) and return the host
+    tensors and an event that marks their completion.
+
+    The side stream first waits for the work already queued on the current
+    stream, so the copies see every earlier write of their sources.  Kernels
+    queued on the current stream afterwards do not wait for the copies: the
+    validation copies stay off the compute stream.  Used where the kernels
+    run many small workgroups (padded, packed), so the copies' blit kernels
+    find a free CU at once."""
+    device = tensors[0].device
+    cur = torch.cuda.current_stream(device)
+    side = _COPY_STREAMS.get(device.index)
+    if side is None:
+        side = _COPY_STREAMS[device.index] = torch.cuda.Stream(device)
+    side.wait_stream(cur)
+    hosts = []
+    with torch.cuda.stream(side):
+        for t in tensors:
+            flat = t.detach().reshape(-1)
+            host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
+            host.copy_(flat, non_blocking=True)
+            hosts.append(host)
+        done = torch.cuda.Event()
+        done.record(side)
+    return hosts, done
+
+
 def _check_lengths(values: np.ndarray, max_len: int, name: str) -> None:
     if (values <= 0).any():
         raise ValueError(f"{name} must contain values > 0")
@@ -162,9 +194,9 @@ def _check_padded_meta(queries, documents, query_lengths, doc_lengths):
 def _checked_padded(queries, documents, query_lengths, doc_lengths, launch):
     """Validate a padded call and return ``launch(B, C, Lq, Ld)``.
 
-    The lengths travel to pinned host memory by asynchronous copies queued
-    ahead of the kernels, ``launch`` queues the kernels, and only then does
-    the host wait for the copies and check the values, with the same errors
+    The lengths travel to pinned host memory by asynchronous copies on a side
+    stream (:func:`_host_copies_async`), ``launch`` queues the kernels, and
+    only then does the host wait for the copies and check the values, with the same errors
     as a check made before the launch.  The padded kernels are safe with any
     lengths (a candidate with a length outside ``(0, Ld]`` or a query length
     outside ``(0, Lq]`` gives a NaN score, nothing is read out of range), so
@@ -176,14 +208,7 @@ def _checked_padded(queries, documents, query_lengths, doc_lengths, launch):
         _check_lengths(qlen, Lq, "query_lengths")
         _check_lengths(dlen, Ld, "doc_lengths")
         return launch(B, C, Lq, Ld)
-    hosts = []
-    for t in (query_lengths, doc_lengths):
-        flat = t.detach().reshape(-1)
-        host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
-        host.copy_(flat, non_blocking=True)
-        hosts.append(host)
-    copied = torch.cuda.Event()
-    copied.record()
+    hosts, copied = _host_copies_async(query_lengths, doc_lengths)
     result = launch(B, C, Lq, Ld)
     copied.synchronize()
     qlen, dlen = (h.numpy().astype(np.int64) for h in hosts)
@@ -244,9 +269,10 @@ def _checked_packed(queries, query_offsets, documents, document_offsets,
 
     Without ``max_q_len`` the output shape depends on the offsets, so they are
     read and checked before anything is launched.  With it, the offsets and
-    ids travel to pinned host memory by asynchronous copies queued ahead of
-    the kernels, ``launch`` queues the kernels, and only then does the host
-    wait for the copies and run the same checks with the same errors.  The
+    ids travel to pinned host memory by asynchronous copies on a side stream
+    (:func:`_host_copies_async`), ``launch`` queues the kernels, and only then
+    does the host wait for the copies and run the same checks with the same
+    errors.  The
     packed kernels are safe with any offsets and ids (an invalid pair gives a
     NaN score, nothing is read out of range), so work queued before a failing
     check is harmless and its result is dropped."""
@@ -256,14 +282,8 @@ def _checked_packed(queries, query_offsets, documents, document_offsets,
             pair_query_ids, pair_document_ids)))
     if max_q_len <= 0:
         raise ValueError(f"max_q_len must be > 0; got {max_q_len}")
-    hosts = []
-    for t in (query_offsets, document_offsets, pair_query_ids, pair_document_ids):
-        flat = t.detach().reshape(-1)
-        host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
-        host.copy_(flat, non_blocking=True)
-        hosts.append(host)
-    copied = torch.cuda.Event()
-    copied.record()
+    hosts, copied = _host_copies_async(query_offsets, document_offsets, pair_query_ids,
+                                       pair_document_ids)
     result = launch(int(max_q_len))
     copied.synchronize()
     qoff, doff, qids, dids = (h.numpy().astype(np.int64) for h in hosts)
@@ -555,6 +575,11 @@ def _checked_contrastive(queries, documents, document_offsets, launch):
     if not flat.is_cuda:  # host tensors: check first (the operators reject them anyway)
         _check_offsets(flat.numpy().astype(np.int64), documents.shape[0])
         return launch()
+    # The copy stays on the current stream: a small copy runs as a blit
+    # kernel, and on a side stream it would wait for a free CU until the
+    # contrastive forward (one large workgroup per CU) ends, keeping the host
+    # from queueing the next launches in time.  In the stream it costs a few
+    # microseconds between the previous step's work and the forward.
     host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
     host.copy_(flat, non_blocking=True)
     copied = torch.cuda.Event()

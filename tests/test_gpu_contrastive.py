@@ -332,3 +332,19 @@ def test_contrastive_decreasing_offsets_overflowing_a_chunk():
     torch.cuda.synchronize()
     assert torch.isnan(scores).all()
     assert torch.all(argmax == 0)
+
+
+def test_contrastive_validation_sees_writes_queued_just_before():
+    """Offsets made invalid by a device write queued right before the call,
+    behind a long kernel, are seen by the overlapped validation and
+    rejected."""
+    q, d, _ = make_contrastive(2, 16, 32, [32, 32, 32, 32], torch.float16, seed=4)
+    off = torch.tensor([0, 32, 64, 96, 128], dtype=torch.int32, device=DEVICE)
+    torch.cuda.synchronize()
+    a = torch.randn(4096, 4096, device=DEVICE)
+    for _ in range(4):
+        a = a @ a / 64.0  # keeps the current stream busy for a while
+    off[2] = -5
+    with pytest.raises(ValueError):
+        maxsim_amd.score_contrastive(q, d, off)
+    torch.cuda.synchronize()

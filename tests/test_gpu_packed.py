@@ -313,3 +313,18 @@ def test_packed_train_grads_in_input_dtype(dtype):
     _, mag_d = ops.maxsim_packed_backward(w.abs(), q.abs(), qoff, d, doff, qids, dids, am, mql)
     assert_rounded_from(qg.grad, dq32, mag_q)
     assert_rounded_from(dg.grad, dd32, mag_d)
+
+
+def test_packed_validation_sees_writes_queued_just_before():
+    """As for the contrastive path: with max_q_len the ids are copied on a
+    side stream that waits for the current one, so an id made invalid just
+    before the call, behind a long kernel, is rejected."""
+    q, qoff, d, doff, qids, dids = make_packed(4, 5, 9, 32, (2, 20), (4, 50), torch.float32, seed=8)
+    torch.cuda.synchronize()
+    a = torch.randn(4096, 4096, device=DEVICE)
+    for _ in range(4):
+        a = a @ a / 64.0
+    dids[3] = 99
+    with pytest.raises(RuntimeError, match="pair_document_ids"):
+        maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids, max_q_len=20)
+    torch.cuda.synchronize()
