@@ -263,35 +263,65 @@ def _packed_layout(queries, query_offsets, documents, document_offsets,
     return max_q
 
 
+def _device_max_segment(offsets: torch.Tensor, total: int):
+    """Longest segment of device CSR offsets, read back as one integer (a
+    small reduction and a one-element copy instead of all the offsets), or
+    None when the offsets cannot be well formed (the host checks then give
+    the error)."""
+    flat = offsets.detach().reshape(-1)
+    if flat.numel() < 2:
+        return None
+    m = int(torch.diff(flat).max())
+    return m if 0 < m <= total else None
+
+
 def _checked_packed(queries, query_offsets, documents, document_offsets,
-                    pair_query_ids, pair_document_ids, max_q_len, launch):
+                    pair_query_ids, pair_document_ids, max_q_len, launch, *,
+                    shape_needs_max=True):
     """Validate a packed call and return ``launch(max_q_len)``.
 
-    Without ``max_q_len`` the output shape depends on the offsets, so they are
-    read and checked before anything is launched.  With it, the offsets and
-    ids travel to pinned host memory by asynchronous copies on a side stream
-    (:func:`_host_copies_async`), ``launch`` queues the kernels, and only then
-    does the host wait for the copies and run the same checks with the same
-    errors.  The
-    packed kernels are safe with any offsets and ids (an invalid pair gives a
-    NaN score, nothing is read out of range), so work queued before a failing
-    check is harmless and its result is dropped."""
-    if max_q_len is None or not query_offsets.is_cuda:
+    The offsets and ids travel to pinned host memory by asynchronous copies
+    on a side stream (:func:`_host_copies_async`), ``launch`` queues the
+    kernels, and only then does the host wait for the copies and run the
+    reference's checks with its errors.  The packed kernels are safe with
+    any offsets and ids (an invalid pair gives a NaN score, nothing is read
+    out of range), so work queued before a failing check is harmless and its
+    result is dropped.
+
+    Without ``max_q_len`` the launch needs a bound of the query lengths.  A
+    score-only call (``shape_needs_max=False``) uses the number of query
+    rows, which bounds every valid segment and gives the same scores.  Where
+    the argmax shape is the longest query, that length is computed on the
+    device and read back as one integer; offsets that cannot be well formed
+    take the synchronous checks first."""
+    if not query_offsets.is_cuda:  # host tensors: check first (the operators reject them)
         return launch(_resolve_max_q_len(max_q_len, _packed_layout(
             queries, query_offsets, documents, document_offsets,
             pair_query_ids, pair_document_ids)))
-    if max_q_len <= 0:
+    if max_q_len is not None and max_q_len <= 0:
         raise ValueError(f"max_q_len must be > 0; got {max_q_len}")
+    # queued before the read-back below, so that only the launch sits
+    # between the host's wait for the longest query and the kernels
     hosts, copied = _host_copies_async(query_offsets, document_offsets, pair_query_ids,
                                        pair_document_ids)
-    result = launch(int(max_q_len))
+    if max_q_len is not None:
+        mql = int(max_q_len)
+    elif not shape_needs_max:
+        mql = max(int(queries.shape[0]), 1)
+    else:
+        mql = _device_max_segment(query_offsets, int(queries.shape[0]))
+        if mql is None:
+            return launch(_packed_layout(queries, query_offsets, documents, document_offsets,
+                                         pair_query_ids, pair_document_ids))
+    result = launch(mql)
     copied.synchronize()
     qoff, doff, qids, dids = (h.numpy().astype(np.int64) for h in hosts)
     max_q = _check_csr(qoff, queries.shape[0], "query_offsets")
     _check_csr(doff, documents.shape[0], "document_offsets")
     _check_ids(qids, qoff.size - 1, "pair_query_ids")
     _check_ids(dids, doff.size - 1, "pair_document_ids")
-    _resolve_max_q_len(max_q_len, max_q)
+    if max_q_len is not None:
+        _resolve_max_q_len(max_q_len, max_q)
     return result
 
 
@@ -423,7 +453,8 @@ def score_pairs_packed(queries, query_offsets, documents, document_offsets,
         lambda mql: ops.maxsim_forward(
             queries.contiguous(), query_offsets.contiguous(), documents.contiguous(),
             document_offsets.contiguous(), pair_query_ids.contiguous(),
-            pair_document_ids.contiguous(), mql))
+            pair_document_ids.contiguous(), mql),
+        shape_needs_max=False)
 
 
 def score_pairs_packed_with_argmax(queries, query_offsets, documents, document_offsets,

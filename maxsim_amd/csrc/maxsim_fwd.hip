@@ -169,9 +169,13 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
     const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
     float score = 0.0f;
     for (int g0 = 0; g0 < nblk; g0 += QB) {
+      // query blocks of this pass that hold tokens (wave-uniform); the last
+      // pass of a query can have fewer than QB
+      const int nact = min(QB, nblk - g0);
       if (pr.q_row0 != loaded_q || pr.lq != loaded_lq || g0 != loaded_g) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
+          if (qb >= nact) break;
           const int tok = min((g0 + qb) * kTileCols + c, pr.lq - 1);
           const S* row = Q + (pr.q_row0 + tok) * (int64_t)dim;
 #pragma unroll
@@ -193,30 +197,40 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
       df_ready = false;
       // after the last tile of the last pass comes the next pair's tile 0
       const bool hand_over = (g0 + QB >= nblk) && nx.ok;
-      for (int t = 0; t < ntiles; ++t) {
-        Frag<T> nf[KS];
-        const bool more = t + 1 < ntiles;
-        if (more)
-          load_tile(pr, t + 1, nf);
-        else if (hand_over)
-          load_tile(nx, 0, nf);
-        // rows past the document end were loaded as copies of its last row
-        // and cannot win (see tile_update), so no masking is needed
-        f32x16 acc[QB];
+      // The tile walk for NA active query blocks: a pass with fewer blocks
+      // than QB (a query of at most 32 tokens under QB = 2) runs no MFMAs and
+      // no epilogue for the empty ones.
+      auto walk = [&](auto na_const) __attribute__((always_inline)) {
+        constexpr int NA = decltype(na_const)::value;
+        for (int t = 0; t < ntiles; ++t) {
+          Frag<T> nf[KS];
+          const bool more = t + 1 < ntiles;
+          if (more)
+            load_tile(pr, t + 1, nf);
+          else if (hand_over)
+            load_tile(nx, 0, nf);
+          // rows past the document end were loaded as copies of its last row
+          // and cannot win (see tile_update), so no masking is needed
+          f32x16 acc[NA];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          acc[qb] = f32x16{};
+          for (int qb = 0; qb < NA; ++qb) {
+            acc[qb] = f32x16{};
 #pragma unroll
-          for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
+            for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
+          }
+#pragma unroll
+          for (int qb = 0; qb < NA; ++qb)
+            tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
+          if (more || hand_over) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) df[s] = nf[s];
+          }
         }
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
-        if (more || hand_over) {
-#pragma unroll
-          for (int s = 0; s < KS; ++s) df[s] = nf[s];
-        }
-      }
+      };
+      if (QB > 1 && nact == 1)
+        walk(std::integral_constant<int, 1>{});
+      else
+        walk(std::integral_constant<int, QB>{});
       df_ready = hand_over;
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {

@@ -204,6 +204,50 @@ def test_packed_bad_device_inputs_with_max_q_len_raise_after_queueing(fn):
     assert_close(s, s_ref, **SCORE_TOL[torch.float16])
 
 
+@pytest.mark.parametrize("fn", PACKED_FNS, ids=lambda f: f.__name__)
+def test_packed_bad_device_inputs_without_max_q_len(fn):
+    """Without max_q_len the score-only call launches with the number of
+    query rows as the length bound and the others read back only the longest
+    query length; the checks then run while the kernels execute, or first
+    when the offsets cannot be well formed.  Every bad input still raises the
+    reference's error."""
+    q, qo, d, do, i32 = _packed_dev()
+    one = torch.tensor([1], **i32)
+    zero = torch.tensor([0], **i32)
+    with pytest.raises(RuntimeError, match="0|offset|start"):
+        fn(q, torch.tensor([1, 5, 13], **i32), d, do, one, zero)
+    with pytest.raises(RuntimeError, match="total|equal|offset"):
+        fn(q, torch.tensor([0, 5, 12], **i32), d, do, one, zero)
+    with pytest.raises(RuntimeError, match="total|equal|offset|decreas|order"):
+        fn(q, torch.tensor([0, 9, 5, 13], **i32), d, do, one, zero)  # a negative segment
+    with pytest.raises(RuntimeError, match="total|equal|offset"):
+        fn(q, qo, d, torch.tensor([0, 30], **i32), one, zero)
+    with pytest.raises(RuntimeError, match="out of range"):
+        fn(q, qo, d, do, torch.tensor([-1], **i32), zero)
+    with pytest.raises(RuntimeError, match="out of range"):
+        fn(q, qo, d, do, one, torch.tensor([7], **i32))
+    torch.cuda.synchronize()
+    s_ref, a_ref = oracle.packed_forward(np64(q), npi(qo), np64(d), npi(do), npi(one), npi(zero), 8)
+    out = fn(q, qo, d, do, one, zero)
+    s = out[0] if isinstance(out, tuple) else out
+    assert_close(s.detach(), s_ref, **SCORE_TOL[torch.float16])
+    if isinstance(out, tuple):
+        assert tuple(out[1].shape) == (1, 8)
+
+
+def test_packed_score_only_bound_gives_identical_scores():
+    """The score-only call without max_q_len launches with the number of
+    query rows as the length bound (two query blocks in registers for every
+    pair); the scores are bit-identical to a launch with the exact longest
+    query length, including queries of at most 32 tokens."""
+    for qr in [(4, 32), (4, 64), (30, 100)]:
+        q, qoff, d, doff, qids, dids = make_packed(9, 13, 60, 128, qr, (8, 300), torch.bfloat16,
+                                                   seed=qr[1])
+        mql = int(np.diff(npi(qoff)).max())
+        exact = ops.maxsim_forward(q, qoff, d, doff, qids, dids, mql)
+        assert torch.equal(maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids), exact)
+
+
 def _typed_vs_fp32(q, qoff, d, doff, qids, dids, seed):
     """Typed packed backward against the fp32 operator cast to the input
     dtype (round to nearest even), up to fp32 summation-order noise; both
