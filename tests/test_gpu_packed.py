@@ -277,6 +277,8 @@ TYPED = [
     pytest.param(5, 7, 13, 20, (1, 64), (1, 64), False, id="dim20-element-wise"),
     pytest.param(7, 13, 900, 64, (4, 40), (8, 300), True, id="hot-document-multi-stage"),
     pytest.param(5, 6, 400, 128, (8, 64), (300, 1000), True, id="hot-long-documents-row-passes"),
+    pytest.param(5, 6, 300, 20, (4, 40), (100, 900), True, id="hot-dim20-element-wise"),
+    pytest.param(4, 5, 300, 256, (4, 48), (70, 200), True, id="hot-dim256-64-row-passes"),
 ]
 
 
