@@ -191,6 +191,11 @@ def _check_padded_meta(queries, documents, query_lengths, doc_lengths):
     return B, C, Lq, Ld, D
 
 
+# The _checked_* wrappers are host code (pinned copies, events, numpy checks);
+# torch.compile runs them eagerly at a graph break, as it does the
+# reference's host-side checks.  The operators they launch have fake
+# implementations and trace on their own.
+@torch.compiler.disable
 def _checked_padded(queries, documents, query_lengths, doc_lengths, launch):
     """Validate a padded call and return ``launch(B, C, Lq, Ld)``.
 
@@ -275,6 +280,7 @@ def _device_max_segment(offsets: torch.Tensor, total: int):
     return m if 0 < m <= total else None
 
 
+@torch.compiler.disable
 def _checked_packed(queries, query_offsets, documents, document_offsets,
                     pair_query_ids, pair_document_ids, max_q_len, launch, *,
                     shape_needs_max=True):
@@ -592,6 +598,7 @@ def score_candidates_padded_train(queries, documents, query_lengths,
 # ---------------------------------------------------------------------------
 # Contrastive (all pairs)
 # ---------------------------------------------------------------------------
+@torch.compiler.disable
 def _checked_contrastive(queries, documents, document_offsets, launch):
     """Validate a contrastive call and return ``launch()``.
 
