@@ -1013,6 +1013,7 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
   __shared__ int32_t st_lq[kPairStage];
   __shared__ int32_t st_p[kPairStage];
   __shared__ float st_g[kPairStage];
+  __shared__ int n_full;  // rows with entries in this stage
   const int64_t di = blockIdx.x;
   const int64_t ds = a.doff[di], de = a.doff[di + 1];
   if (ds < 0 || de <= ds || de > a.total_d) return;
@@ -1052,6 +1053,7 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
         const int ne = nc * tc;
         __syncthreads();
         for (int x = tid; x <= nrows; x += kGroupThreads) start[x] = 0;
+        if (tid == 0) n_full = 0;
         __syncthreads();
         // 1. histogram of target rows
         for (int e = tid; e < ne; e += kGroupThreads) {
@@ -1093,8 +1095,27 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
           if (j >= 0 && j < nrows && j + r0 < ld) ids[atomicAdd(&cursor[j], 1)] = e | (k << 16);
         }
         __syncthreads();
-        // 4. per-row fp32 sums, one group of G lanes per row
-        for (int rr = grp; rr < nrows; rr += ngroups) {
+        // 4. Rows with entries are listed in `cursor` (free after the
+        // scatter); on the first stage the others are zeroed with coalesced
+        // stores (later stages leave them as they are).  Most rows of a short
+        // document have no entry, so the groups then walk only the listed
+        // rows and wait on far fewer gathers.
+        for (int rr = tid; rr < nrows; rr += kGroupThreads)
+          if (start[rr + 1] > start[rr]) cursor[atomicAdd(&n_full, 1)] = rr;
+        if (first) {
+          const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          for (int x = tid; x < nrows * sl_hi; x += kGroupThreads) {
+            const int rr = x / sl_hi;
+            if (start[rr + 1] == start[rr])
+              store8<O>(out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim), (x - rr * sl_hi) * 8, dim,
+                        VEC, zero8);
+          }
+        }
+        __syncthreads();
+        // per-row fp32 sums, one group of G lanes per listed row
+        const int n_rows_full = n_full;
+        for (int i = grp; i < n_rows_full; i += ngroups) {
+          const int rr = cursor[i];
           float acc[NS][8];
           void* dst = out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim);
 #pragma unroll
@@ -1163,8 +1184,9 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
 }
 
 // dd with a 16-bit output type O for the documents dd_packed_kernel leaves
-// (those needing more than one stage of entries); workgroups stride over the
-// documents and skip the others.  Rows are taken
+// (those needing more than one stage of entries).  Workgroups stride over
+// blocks of 256 documents, list the block's documents that need this kernel
+// (one thread per document), and process the listed ones.  Rows are taken
 // kPkAccFloats / dim at a time with their fp32 sums in LDS; a wave adds one
 // entry g_k * q_row at a time (lanes over the embedding dimension, LDS
 // atomics), over every stage of the document's pairs, then each row is
@@ -1181,6 +1203,8 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_multi_kernel(PackedBw
   __shared__ int32_t st_lq[kPairStage];
   __shared__ int32_t st_p[kPairStage];
   __shared__ float st_g[kPairStage];
+  __shared__ int listed[kGroupThreads];
+  __shared__ int n_listed;
   const int dim = a.dim;
   const int slots = a.slots;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1188,57 +1212,71 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_multi_kernel(PackedBw
   const int rows_per_pass = kPkAccFloats / dim;  // >= 64 for dim <= 256
   const S* __restrict__ Q = static_cast<const S*>(a.q);
   uint16_t* __restrict__ out = static_cast<uint16_t*>(a.dd);
-  // di, and so every branch on it, is uniform over the workgroup
-  for (int64_t di = blockIdx.x; di < a.nd; di += gridDim.x) {
-    const int64_t ds = a.doff[di], de = a.doff[di + 1];
-    if (ds < 0 || de <= ds || de > a.total_d) continue;
-    const int k_lo = g.dstart[di], k_hi = g.dstart[di + 1];
-    if (!dd_packed_multi_stage(a, k_hi - k_lo)) continue;
-    const int ld = (int)(de - ds);
-    for (int r0 = 0; r0 < ld; r0 += rows_per_pass) {
-      const int nrows = min(rows_per_pass, ld - r0);
-      const int n_el = nrows * dim;
-      __syncthreads();  // the previous pass has read its sums
-      for (int x = tid; x < n_el; x += kGroupThreads) acc[x] = 0.0f;
-      for (int c0 = k_lo; c0 < k_hi; c0 += kPairStage) {
-        const int nc = min(kPairStage, k_hi - c0);
-        __syncthreads();  // sums zeroed; the previous stage's pairs are no longer read
-        if (tid < nc) {
-          const int p = g.dlist[c0 + tid];
-          const int64_t qi = a.qids[p];
-          const int64_t qs = a.qoff[qi];
-          st_qs[tid] = qs;
-          st_lq[tid] = (int)(a.qoff[qi + 1] - qs);
-          st_p[tid] = p;
-          st_g[tid] = a.dscore[p];
-        }
-        __syncthreads();
-        // entry e = (pair k, token i); one wave per entry, uniform branches
-        const int64_t ne = (int64_t)nc * slots;
-        for (int64_t e = wave; e < ne; e += kWaves) {
-          const int k = (int)(e / slots);
-          const int i = (int)(e - (int64_t)k * slots);
-          if (i >= st_lq[k]) continue;
-          const int jt = a.argmax[(int64_t)st_p[k] * slots + i];
-          if (jt < r0 || jt >= r0 + nrows) continue;
-          const int j = jt - r0;
-          const S* qrow = Q + (st_qs[k] + i) * (int64_t)dim;
-          const float gk = st_g[k];
-          for (int x = lane; x < dim; x += 64) {
-            float v;
-            if constexpr (__is_same(T, BF16))
-              v = __uint_as_float((uint32_t)qrow[x] << 16);
-            else if constexpr (__is_same(T, F16))
-              v = (float)__builtin_bit_cast(_Float16, qrow[x]);
-            else
-              v = qrow[x];
-            atomicAdd(&acc[j * dim + x], gk * v);
+  for (int64_t b0 = (int64_t)blockIdx.x * kGroupThreads; b0 < a.nd;
+       b0 += (int64_t)gridDim.x * kGroupThreads) {
+    __syncthreads();  // the previous block's list and sums are no longer read
+    if (tid == 0) n_listed = 0;
+    __syncthreads();
+    if (b0 + tid < a.nd) {
+      const int64_t di = b0 + tid;
+      const int64_t ds = a.doff[di], de = a.doff[di + 1];
+      if (ds >= 0 && de > ds && de <= a.total_d &&
+          dd_packed_multi_stage(a, g.dstart[di + 1] - g.dstart[di]))
+        listed[atomicAdd(&n_listed, 1)] = tid;
+    }
+    __syncthreads();
+    const int n_docs = n_listed;
+    // di, and so every branch on it, is uniform over the workgroup
+    for (int li = 0; li < n_docs; ++li) {
+      const int64_t di = b0 + listed[li];
+      const int64_t ds = a.doff[di], de = a.doff[di + 1];
+      const int k_lo = g.dstart[di], k_hi = g.dstart[di + 1];
+      const int ld = (int)(de - ds);
+      for (int r0 = 0; r0 < ld; r0 += rows_per_pass) {
+        const int nrows = min(rows_per_pass, ld - r0);
+        const int n_el = nrows * dim;
+        __syncthreads();  // the previous pass has read its sums
+        for (int x = tid; x < n_el; x += kGroupThreads) acc[x] = 0.0f;
+        for (int c0 = k_lo; c0 < k_hi; c0 += kPairStage) {
+          const int nc = min(kPairStage, k_hi - c0);
+          __syncthreads();  // sums zeroed; the previous stage's pairs are no longer read
+          if (tid < nc) {
+            const int p = g.dlist[c0 + tid];
+            const int64_t qi = a.qids[p];
+            const int64_t qs = a.qoff[qi];
+            st_qs[tid] = qs;
+            st_lq[tid] = (int)(a.qoff[qi + 1] - qs);
+            st_p[tid] = p;
+            st_g[tid] = a.dscore[p];
+          }
+          __syncthreads();
+          // entry e = (pair k, token i); one wave per entry, uniform branches
+          const int64_t ne = (int64_t)nc * slots;
+          for (int64_t e = wave; e < ne; e += kWaves) {
+            const int k = (int)(e / slots);
+            const int i = (int)(e - (int64_t)k * slots);
+            if (i >= st_lq[k]) continue;
+            const int jt = a.argmax[(int64_t)st_p[k] * slots + i];
+            if (jt < r0 || jt >= r0 + nrows) continue;
+            const int j = jt - r0;
+            const S* qrow = Q + (st_qs[k] + i) * (int64_t)dim;
+            const float gk = st_g[k];
+            for (int x = lane; x < dim; x += 64) {
+              float v;
+              if constexpr (__is_same(T, BF16))
+                v = __uint_as_float((uint32_t)qrow[x] << 16);
+              else if constexpr (__is_same(T, F16))
+                v = (float)__builtin_bit_cast(_Float16, qrow[x]);
+              else
+                v = qrow[x];
+              atomicAdd(&acc[j * dim + x], gk * v);
+            }
           }
         }
+        __syncthreads();
+        uint16_t* dst = out + (ds + r0) * (int64_t)dim;
+        for (int x = tid; x < n_el; x += kGroupThreads) dst[x] = to_out16<O>(acc[x]);
       }
-      __syncthreads();
-      uint16_t* dst = out + (ds + r0) * (int64_t)dim;
-      for (int x = tid; x < n_el; x += kGroupThreads) dst[x] = to_out16<O>(acc[x]);
     }
   }
 }
@@ -1378,7 +1416,8 @@ static void launch_packed_grouped_o(const PackedBwdArgs& a, const PackedGroups& 
       hipLaunchKernelGGL((dd_packed_kernel<T, false, 1, O>), grid, dim3(kGroupThreads), 0, st, a,
                          g, G);
     if constexpr (O::bytes != 4) {
-      const dim3 grid_m((unsigned)std::min<int64_t>(a.nd, 1024));
+      const dim3 grid_m((unsigned)std::min<int64_t>((a.nd + kGroupThreads - 1) / kGroupThreads,
+                                                    1024));
       hipLaunchKernelGGL((dd_packed_multi_kernel<T, O>), grid_m, dim3(kGroupThreads), 0, st, a,
                          g);
     }
