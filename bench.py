@@ -292,6 +292,17 @@ def main():
                        "hbm_frac": round(bytes3 / (ms3 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
                        "api_ms": round(api3, 3)}
         log(f"C3: {ms3:.3f} ms -> {B * C / (ms3 * 1e-3):.3e} docs/s")
+        # padded -> packed copy of the same candidates (the device work of
+        # _pack_padded): 2 x the valid rows' bytes
+        doff3 = torch.zeros(B * C + 1, dtype=torch.int32, device=dev)
+        doff3[1:] = dlf.cumsum(0)
+        ms_pack = time_events(torch, lambda: ops.maxsim_pack_padded_rows(df, dlf, doff3, Ld, real_rows),
+                              max(3, K // 4), 1)
+        bytes_pack = 2 * 2 * 128 * real_rows
+        extra["c3_pack"] = {"kernel_ms": round(ms_pack, 4),
+                            "gbps": round(bytes_pack / (ms_pack * 1e-3) / 1e9, 1),
+                            "hbm_frac": round(bytes_pack / (ms_pack * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"C3 pack: {ms_pack:.3f} ms, {bytes_pack / (ms_pack * 1e-3) / 1e9:.0f} GB/s")
         del q3, d3, qf, df
         torch.cuda.empty_cache()
 

@@ -230,6 +230,21 @@ int maxsim_amd_contrastive_backward_typed(
     const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- Padded -> packed --------------------------------------------------- */
+
+/* Replaces the boolean-mask gathers of `_pack_padded`
+ * (torch-ext/maxsim/__init__.py:584-593; the whole helper is :516-620).
+ * padded [num_segments * max_len, dim] holds num_segments segments of max_len
+ * rows; segment s contributes its first lengths[s] rows (clamped to
+ * [0, max_len]) to packed [packed_rows, dim] starting at row offsets[s].
+ * The caller computes offsets (the exclusive prefix sum of the lengths) and
+ * allocates packed; rows that would land at or beyond packed_rows are not
+ * written.  Any dim > 0 is accepted (it is a copy). */
+int maxsim_amd_pack_padded_rows(maxsim_dtype dtype, const void* padded, int64_t num_segments,
+                                int64_t max_len, const int32_t* lengths,
+                                const int32_t* offsets, int64_t dim, void* packed,
+                                int64_t packed_rows, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

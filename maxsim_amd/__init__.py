@@ -596,6 +596,72 @@ def score_candidates_padded_train(queries, documents, query_lengths,
 
 
 # ---------------------------------------------------------------------------
+# Padded -> packed
+# ---------------------------------------------------------------------------
+def _pack_padded(queries, documents, query_lengths, doc_lengths, *, validate: bool = False):
+    """Convert padded ``[B, Lq, D]`` / ``[B, C, Ld, D]`` inputs to the packed
+    inputs of :func:`score_pairs_packed` (reference __init__.py:516-620).
+
+    Returns ``(queries_packed, query_offsets, documents_packed,
+    document_offsets, pair_query_ids, pair_document_ids, max_q_len)``; pairs
+    are in row-major ``(batch, candidate)`` order, so the packed scores
+    reshape to ``[B, C]``, and ``max_q_len`` is a Python int.  The valid rows
+    of each query and candidate are one contiguous block of the padded
+    tensor; a HIP kernel copies each block to its packed offset, and one
+    device-to-host copy brings back the two row totals and the longest query
+    (the reference gathers with boolean masks, which sync as well).
+    ``validate=True`` adds the reference's length checks.  Without them,
+    lengths outside ``[0, padded extent]`` are clamped for both the copy and
+    the offsets, so the outputs stay consistent."""
+    if queries.dim() != 3:
+        raise ValueError(f"queries must be 3-D [B, Lq, D]; got shape {tuple(queries.shape)}")
+    if documents.dim() != 4:
+        raise ValueError(
+            f"documents must be 4-D [B, C, Ld, D]; got shape {tuple(documents.shape)}"
+        )
+    B, Lq_max, D = queries.shape
+    Bd, C, Ld_max, Dd = documents.shape
+    if B != Bd:
+        raise ValueError(f"batch dim mismatch: queries B={B} but documents B={Bd}")
+    if D != Dd:
+        raise ValueError(f"embedding dim mismatch: queries D={D} but documents D={Dd}")
+    if query_lengths.shape != (B,):
+        raise ValueError(
+            f"query_lengths must have shape [B={B}]; got {tuple(query_lengths.shape)}"
+        )
+    if doc_lengths.shape != (B, C):
+        raise ValueError(
+            f"doc_lengths must have shape [B={B}, C={C}]; got {tuple(doc_lengths.shape)}"
+        )
+    device = queries.device
+    qlen = query_lengths.to(device=device, dtype=torch.int32)
+    dlen = doc_lengths.to(device=device, dtype=torch.int32)
+    if validate:
+        if (qlen <= 0).any().item():
+            raise ValueError("query_lengths must all be > 0")
+        if (dlen <= 0).any().item():
+            raise ValueError("doc_lengths must all be > 0")
+        if (qlen > Lq_max).any().item() or (dlen > Ld_max).any().item():
+            raise ValueError("a length exceeds the padded extent")
+    qc = qlen.clamp(0, Lq_max)
+    dc = dlen.reshape(-1).clamp(0, Ld_max)
+    query_offsets = torch.zeros(B + 1, dtype=torch.int32, device=device)
+    query_offsets[1:] = qc.cumsum(0)
+    document_offsets = torch.zeros(B * C + 1, dtype=torch.int32, device=device)
+    document_offsets[1:] = dc.cumsum(0)
+    longest = qc.max() if B > 0 else query_offsets[0]
+    total_q, total_d, max_q = (int(x) for x in torch.stack(
+        [query_offsets[-1], document_offsets[-1], longest.to(torch.int32)]).cpu())
+    queries_packed = ops.maxsim_pack_padded_rows(
+        queries.reshape(B * Lq_max, D), qc, query_offsets, Lq_max, total_q)
+    documents_packed = ops.maxsim_pack_padded_rows(
+        documents.reshape(B * C * Ld_max, D), dc, document_offsets, Ld_max, total_d)
+    pair_indices = torch.arange(B * C, dtype=torch.int32, device=device)
+    return (queries_packed, query_offsets, documents_packed, document_offsets,
+            (pair_indices // C).contiguous(), pair_indices.contiguous(), max_q)
+
+
+# ---------------------------------------------------------------------------
 # Contrastive (all pairs)
 # ---------------------------------------------------------------------------
 @torch.compiler.disable

@@ -7,7 +7,8 @@ gfx950 behind the C ABI in ``include/maxsim_amd.h``.  Two more operators,
 ``maxsim_contrastive_backward_typed`` and ``maxsim_packed_backward_typed``,
 are the contrastive and packed backwards with the gradients in the inputs'
 dtype; the autograd Functions use them so that torch does not cast fp32
-gradients in a separate pass.
+gradients in a separate pass.  ``maxsim_pack_padded_rows`` is the device
+copy behind :func:`maxsim_amd._pack_padded` (padded -> packed rows).
 
 Importing this module loads ``_maxsim_amd_torch.so`` (which pulls in
 ``libmaxsim_amd.so``).  There is no fallback: if the native build is missing
@@ -107,6 +108,11 @@ def _(dscore, queries, documents, document_offsets, argmax):
 def _(dscore, queries, query_offsets, documents, document_offsets,
       pair_query_ids, pair_document_ids, argmax, max_q_len):
     return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
+
+
+@torch.library.register_fake("maxsim_amd::maxsim_pack_padded_rows")
+def _(padded, lengths, offsets, max_len, packed_rows):
+    return padded.new_empty((packed_rows, padded.shape[1]))
 
 
 @torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward_typed")

@@ -455,6 +455,35 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_backward_typed(
   return contrastive_backward_impl(dscore, queries, documents, document_offsets, argmax, true);
 }
 
+// ---- padded -> packed -------------------------------------------------------
+
+// Not one of the reference's operators: the device copy behind _pack_padded
+// (torch-ext/maxsim/__init__.py:584-593).  padded [segments * max_len, dim],
+// lengths and offsets [segments] (offsets: exclusive prefix sum of the
+// lengths) -> packed [packed_rows, dim].
+Tensor maxsim_pack_padded_rows(Tensor padded, Tensor lengths, Tensor offsets, int64_t max_len,
+                               int64_t packed_rows) {
+  TORCH_CHECK(padded.device().is_cuda(), "padded must be a HIP (torch 'cuda') tensor");
+  TORCH_CHECK(padded.dim() == 2, "padded must be 2-D [segments * max_len, dim]");
+  TORCH_CHECK(max_len >= 0 && packed_rows >= 0, "max_len and packed_rows must be >= 0");
+  check_on(lengths, padded, "lengths");
+  check_on(offsets, padded, "offsets");
+  Tensor p = padded.contiguous();
+  Tensor len = as_i32(lengths);
+  Tensor off = as_i32(offsets);
+  const int64_t nseg = len.numel();
+  TORCH_CHECK(off.numel() >= nseg, "offsets must have one entry per segment");
+  TORCH_CHECK(p.size(0) == nseg * max_len, "padded must have segments * max_len rows");
+  Tensor out = at::empty({packed_rows, p.size(1)}, p.options());
+  if (nseg == 0 || packed_rows == 0 || max_len == 0) return out;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(p.device());
+  check_status(maxsim_amd_pack_padded_rows(to_dtype(p), p.data_ptr(), nseg, max_len,
+                                           len.data_ptr<int32_t>(), off.data_ptr<int32_t>(),
+                                           p.size(1), out.data_ptr(), packed_rows,
+                                           current_stream(p)));
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(maxsim_amd, m) {
@@ -485,6 +514,8 @@ TORCH_LIBRARY(maxsim_amd, m) {
   m.def("maxsim_packed_backward_typed(Tensor dscore, Tensor queries, Tensor query_offsets, "
         "Tensor documents, Tensor document_offsets, Tensor pair_query_ids, "
         "Tensor pair_document_ids, Tensor argmax, int max_q_len) -> (Tensor, Tensor)");
+  m.def("maxsim_pack_padded_rows(Tensor padded, Tensor lengths, Tensor offsets, int max_len, "
+        "int packed_rows) -> Tensor");
   m.def("maxsim_contrastive_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
         "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
 }
@@ -502,4 +533,5 @@ TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
          &maxsim_contrastive_forward_with_argmax);
   m.impl("maxsim_contrastive_backward", &maxsim_contrastive_backward);
   m.impl("maxsim_contrastive_backward_typed", &maxsim_contrastive_backward_typed);
+  m.impl("maxsim_pack_padded_rows", &maxsim_pack_padded_rows);
 }

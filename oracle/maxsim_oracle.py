@@ -43,6 +43,7 @@ __all__ = [
     "contrastive_backward",
     "padded_backward",
     "packed_backward",
+    "pack_padded",
 ]
 
 
@@ -202,3 +203,26 @@ def packed_backward(dscore, queries, query_offsets, documents, document_offsets,
         np.add.at(dq, rq, g[k] * d[rd])
         np.add.at(dd, rd, g[k] * q[rq])
     return dq.astype(np.float32), dd.astype(np.float32)
+
+
+def pack_padded(queries, documents, query_lengths, doc_lengths):
+    """_pack_padded (torch-ext/maxsim/__init__.py:516-620): padded ``[B, Lq, D]``
+    / ``[B, C, Ld, D]`` -> (queries_packed, query_offsets, documents_packed,
+    document_offsets, pair_query_ids, pair_document_ids, max_q_len).  Rows
+    keep their values (no arithmetic); the valid rows of each query and each
+    candidate, in row-major (b, c) order; offsets are the prefix sums of the
+    lengths; pair k = (b, c) = (k // C, k)."""
+    q = np.asarray(queries)
+    d = np.asarray(documents)
+    ql = np.asarray(query_lengths, dtype=np.int64)
+    dl = np.asarray(doc_lengths, dtype=np.int64)
+    B, Lq, D = q.shape
+    _, C, Ld, _ = d.shape
+    qmask = np.arange(Lq)[None, :] < ql[:, None]
+    dmask = np.arange(Ld)[None, None, :] < dl[:, :, None]
+    qp = q.reshape(B * Lq, D)[qmask.reshape(-1)]
+    dp = d.reshape(B * C * Ld, D)[dmask.reshape(-1)]
+    qo = np.concatenate([[0], np.cumsum(ql)]).astype(np.int64)
+    do = np.concatenate([[0], np.cumsum(dl.reshape(-1))]).astype(np.int64)
+    pairs = np.arange(B * C, dtype=np.int64)
+    return qp, qo, dp, do, pairs // max(C, 1), pairs, int(ql.max()) if B else 0

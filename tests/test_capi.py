@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 15, names
+    assert len(names) == 16, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 5
+    assert lib.maxsim_amd_abi_version() == 6
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -182,3 +182,19 @@ def test_typed_packed_backward_16bit_needs_the_grouped_path(lib):
     assert b"fp32" in lib.maxsim_amd_last_error()
     # max_q_len beyond the 16-bit entry ids of the grouped kernels: refused too
     assert _typed_packed_backward(lib, mql=70000, ws=P(16), ws_bytes=1 << 20) == UNSUPPORTED
+
+
+def test_pack_rejects_bad_arguments(lib):
+    fn = lib.maxsim_amd_pack_padded_rows
+    fn.argtypes = [ctypes.c_int, P, I64, I64, P, P, I64, P, I64, P]
+    one = P(16)
+    assert fn(7, one, 2, 4, one, one, 8, one, 8, None) == INVALID
+    assert fn(F32, one, -1, 4, one, one, 8, one, 8, None) == INVALID
+    assert fn(F32, one, 2, 4, one, one, 0, one, 8, None) == INVALID
+    assert b"dim" in lib.maxsim_amd_last_error()
+    assert fn(F32, None, 2, 4, one, one, 8, one, 8, None) == INVALID
+    assert b"null" in lib.maxsim_amd_last_error()
+    # nothing to copy: success without touching the pointers
+    assert fn(F32, None, 0, 4, None, None, 8, None, 0, None) == OK
+    # more padded bytes per segment than one launch covers
+    assert fn(F32, one, 2, 1 << 28, one, one, 256, one, 8, None) == UNSUPPORTED

@@ -206,10 +206,34 @@ def pin_golden_c1():
     assert np.array_equal(a, gold["argmax"])
 
 
+def pin_pack_padded():
+    """Packing against a row-by-row construction, and scoring the packed pairs
+    against scoring the padded candidates."""
+    rng = np.random.default_rng(23)
+    B, C, Lq, Ld, D = 3, 4, 7, 11, 5
+    q = rng.standard_normal((B, Lq, D))
+    d = rng.standard_normal((B, C, Ld, D))
+    ql = np.array([7, 1, 4])
+    dl = rng.integers(1, Ld + 1, (B, C))
+    qp, qo, dp, do, qi, di, mql = oracle.pack_padded(q, d, ql, dl)
+    assert np.array_equal(qp, np.array([q[b, i] for b in range(B) for i in range(ql[b])]))
+    assert np.array_equal(dp, np.array([d[b, c, j] for b in range(B) for c in range(C)
+                                        for j in range(dl[b, c])]))
+    assert qo.tolist() == [0, 7, 8, 12]
+    lens = [int(dl[b, c]) for b in range(B) for c in range(C)]
+    assert do.tolist() == [sum(lens[:k]) for k in range(B * C + 1)]
+    assert qi.tolist() == [b for b in range(B) for _ in range(C)]
+    assert di.tolist() == list(range(B * C)) and mql == 7
+    sp, ap = oracle.packed_forward(qp, qo, dp, do, qi, di, mql)
+    s, a = oracle.padded_forward(q, d, ql, dl)
+    assert np.array_equal(sp.reshape(B, C), s)
+    assert np.array_equal(ap.reshape(B, C, mql), a)
+
+
 PINS = [pin_single_token, pin_identical_rows_argmax_zero, pin_self_similarity,
         pin_torch_einsum_max, pin_torch_autograd, pin_nan_contract, pin_inf_contract,
         pin_surfaces_agree, pin_pad_garbage_ignored, pin_backward_zero_and_padded_packed,
-        pin_empty_pairs, pin_golden_c1]
+        pin_empty_pairs, pin_golden_c1, pin_pack_padded]
 
 
 @pytest.mark.parametrize("pin", PINS, ids=lambda f: f.__name__)
@@ -270,3 +294,26 @@ def test_backward_mutant_is_caught(monkeypatch):
     monkeypatch.setattr(oracle, "contrastive_backward", shifted)
     with pytest.raises(AssertionError):
         pin_torch_autograd()
+
+
+@pytest.mark.parametrize("mutant", ["candidate_major_pairs", "offsets_shifted", "one_row_short"])
+def test_pack_padded_mutant_is_caught(monkeypatch, mutant):
+    """A packing that orders the pairs candidate-major, shifts the offsets by
+    one segment, or drops a segment's last row must fail the packing pin."""
+    real = oracle.pack_padded
+
+    def broken(q, d, ql, dl):
+        qp, qo, dp, do, qi, di, mql = real(q, d, ql, dl)
+        B, C = np.asarray(dl).shape
+        if mutant == "candidate_major_pairs":
+            k = np.arange(B * C)
+            qi, di = k % B, (k % B) * C + k // B
+        elif mutant == "offsets_shifted":
+            do = np.concatenate([[0], do[:-1]])
+        else:
+            return real(q, d, np.maximum(np.asarray(ql) - 1, 1), dl)
+        return qp, qo, dp, do, qi, di, mql
+
+    monkeypatch.setattr(oracle, "pack_padded", broken)
+    with pytest.raises(AssertionError):
+        pin_pack_padded()
