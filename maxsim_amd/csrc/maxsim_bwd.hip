@@ -992,8 +992,8 @@ __global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs 
 // With a 16-bit output type O, documents that need more than one stage are
 // left to dd_packed_multi_kernel (a 16-bit row cannot hold the partial sum a
 // later stage would add to), so every row written here is written once.
-constexpr int kPkRows = 2048;     // rows bucketed per pass
-constexpr int kPkEntries = 4096;  // entries per stage (bucket ids held in LDS)
+constexpr int kPkRows = 1024;     // rows bucketed per pass
+constexpr int kPkEntries = 2048;  // entries per stage (bucket ids held in LDS)
 
 // True when a document with n_pairs pairs needs more than one stage of
 // entries in dd_packed_kernel.

@@ -27,6 +27,7 @@ CASES = [
     pytest.param(3, 4, 6, 128, (8, 24), (16, 96), id="train-shape"),
     pytest.param(4, 9, 40, 128, (8, 100), (16, 300), id="Lq-up-to-100"),
     pytest.param(2, 3, 5, 24, (3, 9), (5, 40), id="d24"),
+    pytest.param(3, 4, 9, 64, (4, 40), (1100, 2600), id="docs-over-two-row-passes"),
 ]
 
 
@@ -279,6 +280,7 @@ TYPED = [
     pytest.param(5, 6, 400, 128, (8, 64), (300, 1000), True, id="hot-long-documents-row-passes"),
     pytest.param(5, 6, 300, 20, (4, 40), (100, 900), True, id="hot-dim20-element-wise"),
     pytest.param(4, 5, 300, 256, (4, 48), (70, 200), True, id="hot-dim256-64-row-passes"),
+    pytest.param(3, 4, 9, 64, (4, 40), (1100, 2600), False, id="docs-over-two-row-passes"),
 ]
 
 
