@@ -47,7 +47,7 @@ def contrastive_step(q_rows: torch.Tensor, row_ids: torch.Tensor, docs_padded: t
     scores = contrastive_scores(q, d, mask)
     loss = F.cross_entropy(scores, row_ids, reduction="sum") / nq_total
     loss.backward()
-    return float(loss)
+    return float(loss.detach())
 
 
 def padded_scores(q: torch.Tensor, d: torch.Tensor, qlen: torch.Tensor, dlen: torch.Tensor) -> torch.Tensor:
