@@ -50,6 +50,11 @@ def parse_args():
     p.add_argument("--profile-ops", action="store_true",
                    help="run only the C5 operators (3x forward+argmax, 3x backward) and a "
                         "1 GiB device copy, for rocprofv3 counter passes")
+    p.add_argument("--matrix", metavar="OUT_JSON",
+                   help="run the reference's preset matrix (scripts/bench_matrix.py) instead and "
+                        "write its v2 result schema to OUT_JSON")
+    p.add_argument("--matrix-iters", type=int, default=30)
+    p.add_argument("--matrix-repeats", type=int, default=3)
     return p.parse_args()
 
 
@@ -180,6 +185,230 @@ def profile_ops(torch, dev):
     print(json.dumps({"profile_ops": "c5", "copy_bytes": src.numel() * 4}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# Preset matrix in the reference's bench_results/v2 schema
+# (reference scripts/bench_matrix.py:291-545, 649-792): the same presets,
+# timing (per-iteration events around one call, median over iterations, then
+# the median over repeats), pure-PyTorch fp32 baselines, tolerances and
+# fields, so a result file reads side by side with the reference's.
+# ---------------------------------------------------------------------------
+MATRIX_CONTRASTIVE = [("Contrastive", dict(Nq=32, Nb=32, Lq=32, Ld=80, dim=128)),
+                      ("LongDocs", dict(Nq=32, Nb=32, Lq=32, Ld=512, dim=128)),
+                      ("BigBatch", dict(Nq=64, Nb=64, Lq=32, Ld=128, dim=128))]
+MATRIX_PADDED = [("Rerank", dict(B=32, C=50, Lq=32, Ld=180, dim=128)),
+                 ("HeavyRerank", dict(B=32, C=100, Lq=32, Ld=256, dim=128))]
+MATRIX_PACKED = [("PackedRerank", dict(B=32, C=50, Lq=32, Ld=180, dim=128)),
+                 ("PackedHeavyRerank", dict(B=32, C=100, Lq=32, Ld=256, dim=128))]
+
+
+def run_matrix(args, torch, dev):
+    import datetime
+    import gc
+    import maxsim_amd
+
+    def time_step(fn, n_iter, n_warmup):
+        for _ in range(n_warmup):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(n_iter):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        return statistics.median(times)
+
+    def peak_mb(fn):
+        gc.collect()
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
+        fn()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() / 2**20
+
+    def naive_contrastive(q, docs, cu, d_lens):
+        nb, ld = len(d_lens), max(d_lens)
+        padded = docs.new_zeros((nb, ld, q.shape[2]))
+        offs = cu.to(torch.int64).cpu().tolist()
+        for i, n in enumerate(d_lens):
+            padded[i, :n] = docs[offs[i]:offs[i + 1]]
+        sim = torch.einsum("qid,njd->qnij", q.float(), padded.float())
+        return sim.max(dim=-1).values.sum(dim=-1)
+
+    def naive_padded(q, d, qlen, dlen):
+        lq, ld = q.shape[1], d.shape[2]
+        sim = torch.einsum("bid,bcjd->bcij", q.float(), d.float())
+        qm = torch.arange(lq, device=q.device)[None, :] < qlen[:, None]
+        dm = torch.arange(ld, device=q.device)[None, None, :] < dlen[:, :, None]
+        best = sim.masked_fill(~dm[:, :, None, :], float("-inf")).max(dim=-1).values
+        return best.masked_fill(~qm[:, None, :], 0.0).sum(dim=-1)
+
+    def close(a, b):
+        return bool(torch.allclose(a.float(), b.float(), rtol=3e-2, atol=3e-2))
+
+    label = {torch.float16: "fp16", torch.bfloat16: "bf16"}
+    n_iter, n_warm = args.matrix_iters, 5
+
+    def contrastive(name, shape, dtype):
+        g = torch.Generator().manual_seed(1234)
+        Nq, Nb, Lq, Ld, D = shape["Nq"], shape["Nb"], shape["Lq"], shape["Ld"], shape["dim"]
+        q = torch.randn(Nq, Lq, D, generator=g, dtype=dtype).to(dev)
+        docs = torch.randn(Nb * Ld, D, generator=g, dtype=dtype).to(dev)
+        cu = torch.arange(0, (Nb + 1) * Ld, Ld, dtype=torch.int32, device=dev)
+        lens = [Ld] * Nb
+
+        def fresh():
+            return (q.detach().clone().requires_grad_(True),
+                    docs.detach().clone().requires_grad_(True))
+
+        def k_step():
+            a, b = fresh()
+            maxsim_amd.score_contrastive_train(a, b, cu).sum().backward()
+
+        def n_step():
+            a, b = fresh()
+            naive_contrastive(a, b, cu, lens).sum().backward()
+
+        def k_fwd():
+            a, b = fresh()
+            return maxsim_amd.score_contrastive_train(a, b, cu)
+
+        def n_fwd():
+            a, b = fresh()
+            return naive_contrastive(a, b, cu, lens)
+
+        qk, dk = fresh()
+        qn, dn = fresh()
+        maxsim_amd.score_contrastive_train(qk, dk, cu).sum().backward()
+        naive_contrastive(qn, dn, cu, lens).sum().backward()
+        ok = close(qk.grad, qn.grad) and close(dk.grad, dn.grad)
+        return dict(surface="contrastive_train", preset=name,
+                    shape={"Nq": Nq, "Nb": Nb, "Lq": Lq, "Ld": Ld, "D": D}, dtype=label[dtype],
+                    k=time_step(k_step, n_iter, n_warm), n=time_step(n_step, n_iter, n_warm),
+                    kf=time_step(k_fwd, n_iter, n_warm), nf=time_step(n_fwd, n_iter, n_warm),
+                    padded=None, kmb=peak_mb(k_step), nmb=peak_mb(n_step), red=float(Ld),
+                    correct=ok)
+
+    def padded_inputs(shape, dtype):
+        g = torch.Generator().manual_seed(1234)
+        B, C, Lq, Ld, D = shape["B"], shape["C"], shape["Lq"], shape["Ld"], shape["dim"]
+        q = torch.randn(B, Lq, D, generator=g, dtype=dtype).to(dev)
+        d = torch.randn(B, C, Ld, D, generator=g, dtype=dtype).to(dev)
+        qlen = torch.full((B,), Lq, dtype=torch.int32, device=dev)
+        dlen = torch.full((B, C), Ld, dtype=torch.int32, device=dev)
+        return q, d, qlen, dlen, {"B": B, "K": C, "Lq": Lq, "Ld": Ld, "D": D}
+
+    def padded(name, shape, dtype):
+        q, d, qlen, dlen, sh = padded_inputs(shape, dtype)
+
+        def k_step():
+            return maxsim_amd.score_candidates_padded(q, d, qlen, dlen)
+
+        def n_step():
+            return naive_padded(q, d, qlen, dlen)
+
+        ok = close(k_step(), n_step())
+        return dict(surface="padded_infer", preset=name, shape=sh, dtype=label[dtype],
+                    k=time_step(k_step, n_iter, n_warm), n=time_step(n_step, n_iter, n_warm),
+                    kf=None, nf=None, padded=None, kmb=peak_mb(k_step), nmb=peak_mb(n_step),
+                    red=None, correct=ok)
+
+    def packed(name, shape, dtype):
+        q, d, qlen, dlen, sh = padded_inputs(shape, dtype)
+        B, C, Lq, Ld, D = sh["B"], sh["K"], sh["Lq"], sh["Ld"], sh["D"]
+        qf, df = q.reshape(B * Lq, D).contiguous(), d.reshape(B * C * Ld, D).contiguous()
+        qoff = torch.arange(0, (B + 1) * Lq, Lq, dtype=torch.int32, device=dev)
+        doff = torch.arange(0, (B * C + 1) * Ld, Ld, dtype=torch.int32, device=dev)
+        dids = torch.arange(B * C, dtype=torch.int32, device=dev)
+        qids = dids // C
+
+        def k_step():
+            return maxsim_amd.score_pairs_packed(qf, qoff, df, doff, qids, dids, max_q_len=Lq)
+
+        def n_step():
+            return naive_padded(q, d, qlen, dlen)
+
+        def p_step():
+            return maxsim_amd.score_candidates_padded(q, d, qlen, dlen)
+
+        sk = k_step().view(B, C)
+        ok = close(sk, p_step()) and close(sk, n_step())
+        return dict(surface="packed_infer", preset=name, shape=sh, dtype=label[dtype],
+                    k=time_step(k_step, n_iter, n_warm), n=time_step(n_step, n_iter, n_warm),
+                    kf=None, nf=None, padded=time_step(p_step, n_iter, n_warm),
+                    kmb=peak_mb(k_step), nmb=peak_mb(n_step), red=None, correct=ok)
+
+    def one_matrix():
+        rs = []
+        for dtype in (torch.float16, torch.bfloat16):
+            rs += [contrastive(n, s, dtype) for n, s in MATRIX_CONTRASTIVE]
+            rs += [padded(n, s, dtype) for n, s in MATRIX_PADDED]
+            rs += [packed(n, s, dtype) for n, s in MATRIX_PACKED]
+            log(f"matrix: {label[dtype]} done")
+        return rs
+
+    started = datetime.datetime.now(datetime.timezone.utc)
+    t0 = time.perf_counter()
+    runs = [one_matrix() for _ in range(args.matrix_repeats)]
+    wall = time.perf_counter() - t0
+
+    def med(vals):
+        vals = [v for v in vals if v is not None]
+        return statistics.median(vals) if vals else None
+
+    def ratio(a, b):
+        return a / b if a is not None and b not in (None, 0) else None
+
+    results = []
+    for w in range(len(runs[0])):
+        per = [r[w] for r in runs]
+        base = per[0]
+        k, n = med([r["k"] for r in per]), med([r["n"] for r in per])
+        kf, nf = med([r["kf"] for r in per]), med([r["nf"] for r in per])
+        kb = max(k - kf, 0.0) if kf is not None else None
+        nb = max(n - nf, 0.0) if nf is not None else None
+        kmb, nmb = med([r["kmb"] for r in per]), med([r["nmb"] for r in per])
+        speedups = [r["n"] / r["k"] for r in per]
+        variance = ({"step_speedup_min": min(speedups), "step_speedup_max": max(speedups),
+                     "step_speedup_spread": max(speedups) - min(speedups),
+                     "step_speedup_stdev": statistics.stdev(speedups), "n_repeats": len(per)}
+                    if len(per) >= 2 else {"n_repeats": len(per)})
+        results.append({
+            "surface": base["surface"], "preset": base["preset"], "description": "",
+            "shape": base["shape"], "dtype": base["dtype"],
+            "maxsim_step_ms": k, "naive_step_ms": n, "step_speedup": ratio(n, k),
+            "maxsim_fwd_ms": kf, "naive_fwd_ms": nf,
+            "padded_ms": med([r["padded"] for r in per]),
+            "maxsim_bwd_ms": kb, "naive_bwd_ms": nb, "bwd_speedup": ratio(nb, kb),
+            "maxsim_peak_mb": kmb, "naive_peak_mb": nmb, "peak_ratio": ratio(nmb, kmb),
+            "retained_reduction": base["red"], "correct": all(r["correct"] for r in per),
+            "note": "", "variance": variance,
+        })
+    props = torch.cuda.get_device_properties(dev)
+    payload = {
+        "schema_version": 1,
+        "kernel": {"repo": "maxsim-mi355x", "version": 2, "git_commit": "unknown",
+                   "git_dirty": False},
+        "machine": {"gpu_name": torch.cuda.get_device_name(dev),
+                    "compute_capability": getattr(props, "gcnArchName", "gfx950"),
+                    "torch_version": torch.__version__,
+                    "cuda_version": getattr(torch.version, "hip", None)},
+        "bench": {"iters_per_repeat": n_iter, "warmup": n_warm, "repeats": args.matrix_repeats,
+                  "started_at": started.strftime("%Y-%m-%dT%H:%M:%SZ"),
+                  "wall_seconds": round(wall, 1)},
+        "results": results,
+    }
+    with open(args.matrix, "w") as f:
+        f.write(json.dumps(payload, indent=2) + "\n")
+    log(f"matrix: wrote {args.matrix}")
+    for r in results:
+        log(f"{r['surface']:18s} {r['preset']:18s} {r['dtype']}  maxsim {r['maxsim_step_ms']:.4f} ms  "
+            f"naive {r['naive_step_ms']:.4f} ms  correct {r['correct']}")
+    return 0 if all(r["correct"] for r in results) else 1
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -196,6 +425,8 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.matrix:
+        sys.exit(run_matrix(args, torch, dev))
     if args.profile_ops:
         profile_ops(torch, dev)
         return
