@@ -661,6 +661,28 @@ def _pack_padded(queries, documents, query_lengths, doc_lengths, *, validate: bo
             (pair_indices // C).contiguous(), pair_indices.contiguous(), max_q)
 
 
+def pack_documents(doc_emb, doc_lengths):
+    """Pack padded documents ``[Nb, Ld, D]`` with lengths ``[Nb]`` into the
+    ``(documents [total, D], document_offsets [Nb + 1] int32)`` inputs of the
+    contrastive functions: the device form of the ``torch.cat`` of valid rows
+    and offset prefix sum that callers write before a contrastive call
+    (reference README.md:184-191).  Not in ``__all__``, which stays the
+    reference's list.  One HIP copy per document; lengths are
+    clamped to ``[0, Ld]`` and one device-to-host copy brings back the total
+    row count (the output size)."""
+    if doc_emb.dim() != 3:
+        raise ValueError(f"doc_emb must be 3-D [Nb, Ld, D]; got shape {tuple(doc_emb.shape)}")
+    Nb, Ld, D = doc_emb.shape
+    if doc_lengths.shape != (Nb,):
+        raise ValueError(f"doc_lengths must have shape [Nb={Nb}]; got {tuple(doc_lengths.shape)}")
+    lens = doc_lengths.to(device=doc_emb.device, dtype=torch.int32).clamp(0, Ld)
+    offsets = torch.zeros(Nb + 1, dtype=torch.int32, device=doc_emb.device)
+    offsets[1:] = lens.cumsum(0)
+    total = int(offsets[-1])
+    packed = ops.maxsim_pack_padded_rows(doc_emb.reshape(Nb * Ld, D), lens, offsets, Ld, total)
+    return packed, offsets
+
+
 # ---------------------------------------------------------------------------
 # Contrastive (all pairs)
 # ---------------------------------------------------------------------------

@@ -117,3 +117,22 @@ def test_pack_operator_respects_packed_capacity():
     torch.cuda.synchronize()
     assert out.shape == (4, dim)
     assert torch.equal(out[:2], padded[0:2]) and torch.equal(out[2:4], padded[5:7])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_pack_documents_matches_cat_and_feeds_contrastive(dtype):
+    """pack_documents equals the torch.cat of valid rows plus the prefix-sum
+    offsets that callers build by hand (reference README.md:184-191), bit for
+    bit, and scoring against it equals scoring against the hand-packed form."""
+    g = torch.Generator().manual_seed(17)
+    Nb, Ld, D = 9, 70, 64
+    emb = torch.randn(Nb, Ld, D, generator=g).to(dtype).to(DEVICE)
+    lens = torch.randint(1, Ld + 1, (Nb,), generator=g).to(DEVICE)
+    docs, offs = maxsim_amd.pack_documents(emb, lens)
+    ref_docs = torch.cat([emb[i, :int(lens[i])] for i in range(Nb)], dim=0)
+    ref_offs = torch.zeros(Nb + 1, dtype=torch.int32, device=DEVICE)
+    ref_offs[1:] = lens.cumsum(0)
+    assert torch.equal(docs, ref_docs) and torch.equal(offs, ref_offs)
+    q = torch.randn(5, 32, D, generator=g).to(dtype).to(DEVICE)
+    assert torch.equal(maxsim_amd.score_contrastive(q, docs, offs),
+                       maxsim_amd.score_contrastive(q, ref_docs, ref_offs))
