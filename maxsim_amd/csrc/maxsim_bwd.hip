@@ -1339,13 +1339,35 @@ static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduc
     hipLaunchKernelGGL(dq_reduce_kernel<F32>, grid, dim3(256), 0, st, ws, a.dq, n, vec_reduce);
 }
 
+// Largest dynamic LDS allocation one workgroup may use on the current
+// device, queried once per device (64 KB if the query fails).
+static size_t max_lds_per_block() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+  if (cached[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        v <= 0)
+      v = 64 * 1024;
+    cached[dev] = v;
+  }
+  return (size_t)cached[dev];
+}
+
 template <typename T, bool VEC, int NS, typename O>
 static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st) {
   const auto kern = dd_contrastive_kernel<T, VEC, NS, O>;
   if (lds > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
-    (void)hipGetLastError();
+    // once per device and instantiation: allow up to the device's maximum
+    static bool raised[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !raised[dev]) {
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)max_lds_per_block());
+      (void)hipGetLastError();
+      if (dev >= 0 && dev < 64) raised[dev] = true;
+    }
   }
   const int64_t per_part = kXcds / a.parts;
   const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
@@ -1370,16 +1392,6 @@ static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, bool ou
     launch_dd_contrastive_o<T, T>(a, vec, lds, st);
   else
     launch_dd_contrastive_o<T, F32>(a, vec, lds, st);
-}
-
-// Largest dynamic LDS allocation one workgroup may use on this device.
-static size_t max_lds_per_block() {
-  int dev = 0, v = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 64 * 1024;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
-      v <= 0)
-    return 64 * 1024;
-  return (size_t)v;
 }
 
 template <typename T>
