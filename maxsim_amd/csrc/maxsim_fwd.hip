@@ -792,8 +792,10 @@ static void launch_pair(const FwdArgs& a, int max_lq, int ppw, bool vec,
 }
 
 static int pairs_per_wave(int64_t npairs) {
-  // Aim for ~8k waves (32 per CU) so the chip stays full; never below 1.
-  int64_t ppw = (npairs + 8191) / 8192;
+  // Aim for ~16k waves (64 per CU, several rounds of the 8 resident per CU
+  // at the two-block kernel's register use) so the last round is a small
+  // part of the launch; never below 1.
+  int64_t ppw = (npairs + 16383) / 16384;
   if (ppw < 1) ppw = 1;
   if (ppw > 64) ppw = 64;
   return (int)ppw;
