@@ -123,3 +123,67 @@ def test_packed_backward_with_and_without_workspace(lib):
         assert_close(dd, dd_ref, **GRAD_TOL[torch.bfloat16])
     torch.testing.assert_close(out[0][0], out[1][0], rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(out[0][1], out[1][1], rtol=1e-5, atol=1e-5)
+
+
+def test_packed_backward_typed_through_the_abi(lib):
+    """maxsim_amd_packed_backward_typed with bf16 gradients writes every row
+    of NaN-filled buffers with the oracle's gradients (to bf16 rounding);
+    without a workspace it returns ERR_UNSUPPORTED before writing anything."""
+    from ._helpers import make_packed
+
+    q, qoff, d, doff, qids, dids = make_packed(7, 11, 90, 128, (4, 40), (8, 300),
+                                               torch.bfloat16, seed=21)
+    _, am = maxsim_amd.score_pairs_packed_with_argmax(q, qoff, d, doff, qids, dids)
+    mql = am.shape[1]
+    g = torch.randn(90, generator=torch.Generator().manual_seed(5)).to(DEVICE)
+    fn = lib.maxsim_amd_packed_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, P, I64, P, I64, P, I64, P, P, I64, P,
+                   I64, I64, P, P, P, SZ, P]
+    lib.maxsim_amd_packed_backward_workspace_size.restype = SZ
+    lib.maxsim_amd_packed_backward_workspace_size.argtypes = [I64, I64, I64]
+    need = lib.maxsim_amd_packed_backward_workspace_size(7, 11, 90)
+    ws = torch.empty(need // 4 + 1, dtype=torch.int32, device=DEVICE)
+
+    def call(w, nbytes):
+        dq = torch.full((q.shape[0], 128), float("nan"), dtype=torch.bfloat16, device=DEVICE)
+        dd = torch.full((d.shape[0], 128), float("nan"), dtype=torch.bfloat16, device=DEVICE)
+        rc = fn(DT[q.dtype], DT[torch.bfloat16], g.data_ptr(), q.data_ptr(), q.shape[0],
+                qoff.data_ptr(), 7, d.data_ptr(), d.shape[0], doff.data_ptr(), 11,
+                qids.data_ptr(), dids.data_ptr(), 90, am.data_ptr(), mql, 128, dq.data_ptr(),
+                dd.data_ptr(), w, nbytes, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return rc, dq, dd
+
+    rc, dq, dd = call(None, 0)
+    assert rc == 2 and b"fp32" in lib.maxsim_amd_last_error()
+    assert torch.isnan(dq.float()).all() and torch.isnan(dd.float()).all()
+    rc, dq, dd = call(ws.data_ptr(), need)
+    assert rc == 0, lib.maxsim_amd_last_error()
+    dq_ref, dd_ref = oracle.packed_backward(np64(g), np64(q), npi(qoff), np64(d), npi(doff),
+                                            npi(qids), npi(dids), npi(am))
+    assert_close(dq, dq_ref, rtol=1e-2, atol=1e-2)
+    assert_close(dd, dd_ref, rtol=1e-2, atol=1e-2)
+
+
+def test_pack_padded_rows_through_the_abi(lib):
+    """maxsim_amd_pack_padded_rows copies each segment's first rows to its
+    offset, bit for bit, and leaves rows past the written ones untouched."""
+    fn = lib.maxsim_amd_pack_padded_rows
+    fn.argtypes = [ctypes.c_int, P, I64, I64, P, P, I64, P, I64, P]
+    nseg, max_len, dim = 6, 9, 24
+    padded = torch.randn(nseg * max_len, dim, generator=torch.Generator().manual_seed(3)).to(
+        torch.bfloat16).to(DEVICE)
+    lens = torch.tensor([9, 1, 4, 7, 2, 5], dtype=torch.int32, device=DEVICE)
+    offs = torch.zeros(nseg, dtype=torch.int32, device=DEVICE)
+    offs[1:] = lens.cumsum(0)[:-1]
+    total = int(lens.sum())
+    out = torch.full((total + 3, dim), float("nan"), dtype=torch.bfloat16, device=DEVICE)
+    rc = fn(DT[torch.bfloat16], padded.data_ptr(), nseg, max_len, lens.data_ptr(),
+            offs.data_ptr(), dim, out.data_ptr(), total + 3,
+            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.maxsim_amd_last_error()
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(s * max_len, s * max_len + int(n))
+                      for s, n in enumerate(lens.tolist())]).to(DEVICE)
+    assert torch.equal(out[:total].view(torch.int16), padded[rows].view(torch.int16))
+    assert torch.isnan(out[total:].float()).all()
