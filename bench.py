@@ -37,7 +37,7 @@ PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 # WRITE_SIZE per dispatch, each scaled by the reading for a 1 GiB copy:
 # x3.813 and x1.952).  Counters cannot be read from inside this process, so
 # the figure is the committed measurement, not a live one.
-FWD_TRAFFIC_BYTES_C5 = int((52936.7 * 3.813 + 33888.4 * 1.952) * 1024)
+FWD_TRAFFIC_BYTES_C5 = int((52934.4 * 3.813 + 33888.3 * 1.952) * 1024)
 
 
 def parse_args():
