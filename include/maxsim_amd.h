@@ -168,6 +168,20 @@ int maxsim_amd_padded_backward(
     int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
     float* dqueries, float* ddocuments, void* stream);
 
+/* maxsim_amd_padded_backward with the gradients written in `grad_dtype`:
+ * MAXSIM_FLOAT32, or the input dtype, in which case each element is the fp32
+ * sum rounded to nearest even -- bit for bit what casting the fp32
+ * gradients would give.  No counterpart in the reference: its autograd
+ * Function (torch-ext/maxsim/__init__.py:752-771) returns fp32 gradients
+ * that autograd casts in a separate pass.  Every size the fp32 form accepts
+ * is accepted. */
+int maxsim_amd_padded_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    const void* documents, const int32_t* query_lengths,
+    const int32_t* doc_lengths, const int32_t* argmax, int64_t batch,
+    int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
+    void* dqueries, void* ddocuments, void* stream);
+
 /* ---- Contrastive (all pairs) -------------------------------------------- */
 
 /* Replaces op `maxsim_contrastive_forward` (torch_binding.h:133-135,

@@ -14,9 +14,9 @@ Every function validates its inputs on the host with the reference's error
 types and messages, then calls an operator of :mod:`maxsim_amd._ops`, which
 runs hand-written HIP kernels (fused MFMA forward with an in-register
 max/argmax epilogue; argmax-driven gather/scatter backward).  Scores are fp32;
-gradients are summed in fp32.  ``.grad`` has the input dtype: the padded
-Function returns fp32 gradients that autograd casts, the contrastive and
-packed Functions have the kernels write that rounding (nearest even) directly.
+gradients are summed in fp32.  ``.grad`` has the input dtype: the kernels
+round the fp32 sums to nearest even on the way out, the bits autograd's cast
+of fp32 gradients would give, without the separate cast pass.
 
 The pure-PyTorch ``*_reference`` functions of the reference package are
 exported too (:mod:`maxsim_amd.reference`) for benchmarks and comparisons;
@@ -581,7 +581,8 @@ class _PaddedFn(torch.autograd.Function):
     def backward(ctx, dscore):
         B, C, Lq, Ld, D = ctx.shapes
         q, d, ql, dl, argmax = ctx.saved_tensors
-        dq, dd = ops.maxsim_padded_backward(
+        # gradients in the inputs' dtype, rounded from the fp32 sums
+        dq, dd = ops.maxsim_padded_backward_typed(
             dscore.reshape(B * C).contiguous().to(torch.float32), q, d, ql, dl,
             argmax, int(Lq), int(Ld), int(C))
         return dq.view(B, Lq, D), dd.view(B, C, Ld, D), None, None

@@ -110,6 +110,12 @@ def _(dscore, queries, query_offsets, documents, document_offsets,
     return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
 
 
+@torch.library.register_fake("maxsim_amd::maxsim_padded_backward_typed")
+def _(dscore, queries, documents, query_lengths, doc_lengths, argmax, Lq_max,
+      Ld_max, num_candidates):
+    return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
+
+
 @torch.library.register_fake("maxsim_amd::maxsim_pack_padded_rows")
 def _(padded, lengths, offsets, max_len, packed_rows):
     return padded.new_empty((packed_rows, padded.shape[1]))

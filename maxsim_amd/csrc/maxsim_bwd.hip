@@ -168,7 +168,7 @@ struct DqArgs {
   const void* q;  // unused by the gather itself (kept for symmetry)
   const void* d;
   const int32_t* argmax;
-  void* dq;       // fp32, or the input's 16-bit type (contrastive only)
+  void* dq;       // fp32, or the input's 16-bit type
   int dim;
   int nslices;
   int64_t rows;   // total query rows (Nq*Lq or B*Lq_max)
@@ -676,7 +676,10 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dd, padded: one wave per (query b, candidate c) document.
+// dd, padded: a candidate's rows are split over nsplit waves (one candidate
+// alone is too little work per wave when B*C is small); each wave writes its
+// rows, zeros included, and adds its tokens in token order, so the result is
+// deterministic and does not depend on the split.
 // ---------------------------------------------------------------------------
 struct PaddedDdArgs {
   const float* dscore;
@@ -684,44 +687,173 @@ struct PaddedDdArgs {
   const int32_t* argmax;
   const int32_t* qlen;
   const int32_t* dlen;
-  float* dd;
+  void* dd;  // fp32, or the 16-bit output type O
   int64_t npairs;
   int64_t ncand;
   int lq_max;
   int ld_max;
   int dim;
+  int pair;    // 16-bit O: dim even, q and dd 4-byte aligned (32-bit accesses)
+  int am_lds;  // 16-bit O: argmax ints per wave staged in LDS (0: none)
+  int nsplit;  // waves per candidate, each owning rows_per_split rows
+  int rows_per_split;
 };
 
+// Element x of query row qrow as fp32.
 template <typename T>
+__device__ __forceinline__ float elem_f32(const typename T::storage* qrow, int x) {
+  if constexpr (T::bytes == 4) {
+    return qrow[x];
+  } else if constexpr (__is_same(T, BF16)) {
+    return __uint_as_float((uint32_t)qrow[x] << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, qrow[x]);
+  }
+}
+
+// 16-bit O: each row of the candidate is written once.  For row r the wave
+// ballots the query tokens whose argmax is r (64 tokens at a time) and sums
+// g * q_t over them in token order, from zero, with the same fmaf sequence as
+// the fp32 path below, then rounds: the bits are those of the fp32 gradient
+// cast to O.  Rows no token points at, padding rows and the rows of an
+// invalid candidate are zero.
+//
+// Each lane owns 4 elements of a row: with a.pair, elements 2*lane, +1 and
+// 128 + 2*lane, +1 (32-bit loads and stores), else lane + 64*i.  The argmax
+// of the first 256 tokens is kept in registers and the rest, when a.am_lds
+// is set, in this wave's am_lds slice, so the row loop reads no global memory
+// for it; otherwise tokens past 256 are read again for every row.
+constexpr int kDdAmRegs = 4;
+constexpr int kDdAmLdsMax = 4096;  // ints per wave: 64 KB for the 4 waves
+
+template <typename T, typename O>
+__device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t p, int64_t b,
+                                                 int r0, int r1, int lane, int32_t* am_lds) {
+  using S = typename T::storage;
+  uint16_t* base = static_cast<uint16_t*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
+  const int lqb = a.qlen[b];
+  const int ld = a.dlen[p];
+  const bool ok = lqb >= 1 && lqb <= a.lq_max && ld >= 1 && ld <= a.ld_max;
+  const float g = a.dscore[p];
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const int32_t* am = a.argmax + p * a.lq_max;
+  int amv[kDdAmRegs];
+#pragma unroll
+  for (int c = 0; c < kDdAmRegs; ++c) {
+    const int t = 64 * c + lane;
+    amv[c] = ok && t < lqb ? am[t] : -1;
+  }
+  if (a.am_lds) {
+    if (ok)
+      for (int t = 64 * kDdAmRegs + lane; t < lqb; t += 64) am_lds[t - 64 * kDdAmRegs] = am[t];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  int xs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    xs[i] = a.pair ? 128 * (i >> 1) + 2 * lane + (i & 1) : lane + 64 * i;
+  for (int r = r0; r < r1; ++r) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (ok && r < ld) {
+      for (int c0 = 0; c0 < lqb; c0 += 64) {
+        const int t = c0 + lane;
+        int j = -1;
+        if (c0 < 64 * kDdAmRegs) {
+#pragma unroll
+          for (int c = 0; c < kDdAmRegs; ++c)
+            if (c0 == 64 * c) j = amv[c];
+        } else if (t < lqb) {
+          j = a.am_lds ? am_lds[t - 64 * kDdAmRegs] : am[t];
+        }
+        uint64_t hits = __ballot(j == r);
+        while (hits) {
+          const int tok = c0 + __builtin_ctzll(hits);
+          hits &= hits - 1;
+          const S* qrow = Q + (b * a.lq_max + tok) * (int64_t)a.dim;
+          if (a.pair) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int x = xs[2 * h];
+              if (x < a.dim) {
+                float v0, v1;
+                if constexpr (T::bytes == 4) {
+                  v0 = qrow[x];
+                  v1 = qrow[x + 1];
+                } else {
+                  const uint32_t w = *reinterpret_cast<const uint32_t*>(qrow + x);
+                  v0 = elem_f32<T>(reinterpret_cast<const S*>(&w), 0);
+                  v1 = elem_f32<T>(reinterpret_cast<const S*>(&w), 1);
+                }
+                acc[2 * h] = fmaf(g, v0, acc[2 * h]);
+                acc[2 * h + 1] = fmaf(g, v1, acc[2 * h + 1]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (xs[i] < a.dim) acc[i] = fmaf(g, elem_f32<T>(qrow, xs[i]), acc[i]);
+          }
+        }
+      }
+    }
+    uint16_t* row = base + (int64_t)r * a.dim;
+    if (a.pair) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int x = xs[2 * h];
+        if (x < a.dim)
+          *reinterpret_cast<uint32_t*>(row + x) =
+              (uint32_t)to_out16<O>(acc[2 * h]) | ((uint32_t)to_out16<O>(acc[2 * h + 1]) << 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (xs[i] < a.dim) row[xs[i]] = to_out16<O>(acc[i]);
+    }
+  }
+}
+
+template <typename T, typename O>
 __global__ __launch_bounds__(256) void dd_padded_kernel(PaddedDdArgs a) {
   using S = typename T::storage;
   const int lane = threadIdx.x & 63;
-  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t p = w / a.nsplit;
   if (p >= a.npairs) return;
   const int64_t b = p / a.ncand;
-  float* base = a.dd + p * a.ld_max * (int64_t)a.dim;
-  const int64_t n = (int64_t)a.ld_max * a.dim;
-  for (int64_t x = lane; x < n; x += 64) base[x] = 0.0f;
+  // this wave's rows of candidate p
+  const int r0 = (int)(w - p * a.nsplit) * a.rows_per_split;
+  const int r1 = min(a.ld_max, r0 + a.rows_per_split);
+  if (r0 >= r1) return;
+  if constexpr (O::bytes != 4) {
+    extern __shared__ int32_t dd_am_lds[];
+    dd_padded_rows16<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
+    return;
+  }
+  float* base = static_cast<float*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
+  // zeroed with the lane mapping of the adds below, so each element's zero and
+  // its adds come from one lane in program order
+  for (int r = r0; r < r1; ++r)
+    for (int x = lane; x < a.dim; x += 64) base[(int64_t)r * a.dim + x] = 0.0f;
   const int lqb = a.qlen[b];
   const int ld = a.dlen[p];
   if (lqb < 1 || lqb > a.lq_max || ld < 1 || ld > a.ld_max) return;
   const float g = a.dscore[p];
   const S* __restrict__ Q = static_cast<const S*>(a.q);
-  for (int i = 0; i < lqb; ++i) {
-    const int j = a.argmax[p * a.lq_max + i];
-    if (j < 0 || j >= ld) continue;
-    const S* qrow = Q + (b * a.lq_max + i) * (int64_t)a.dim;
-    float* drow = base + (int64_t)j * a.dim;
-    for (int x = lane; x < a.dim; x += 64) {
-      float qv;
-      if constexpr (T::bytes == 4) {
-        qv = qrow[x];
-      } else if constexpr (__is_same(T, BF16)) {
-        qv = __uint_as_float((uint32_t)qrow[x] << 16);
-      } else {
-        qv = (float)__builtin_bit_cast(_Float16, qrow[x]);
-      }
-      drow[x] = fmaf(g, qv, drow[x]);
+  // argmax 64 tokens at a time, one per lane; the tokens that land in this
+  // wave's rows are then added in token order
+  for (int c0 = 0; c0 < lqb; c0 += 64) {
+    const int jl = c0 + lane < lqb ? a.argmax[p * a.lq_max + c0 + lane] : -1;
+    uint64_t hits = __ballot(jl >= r0 && jl < r1 && jl < ld);
+    while (hits) {
+      const int t = __builtin_ctzll(hits);
+      hits &= hits - 1;
+      const int j = __builtin_amdgcn_readlane(jl, t);
+      const S* qrow = Q + (b * a.lq_max + c0 + t) * (int64_t)a.dim;
+      float* drow = base + (int64_t)j * a.dim;
+      for (int x = lane; x < a.dim; x += 64) drow[x] = fmaf(g, elem_f32<T>(qrow, x), drow[x]);
     }
   }
 }
@@ -1395,9 +1527,16 @@ static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, bool ou
 }
 
 template <typename T>
-static void launch_dd_padded(const PaddedDdArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.npairs + 3) / 4));
-  hipLaunchKernelGGL(dd_padded_kernel<T>, grid, dim3(256), 0, st, a);
+static void launch_dd_padded(const PaddedDdArgs& a, bool out16, hipStream_t st) {
+  const dim3 grid((unsigned)((a.npairs * a.nsplit + 3) / 4));
+  if constexpr (T::bytes == 2) {
+    if (out16) {
+      const size_t lds = (size_t)4 * a.am_lds * sizeof(int32_t);
+      hipLaunchKernelGGL((dd_padded_kernel<T, T>), grid, dim3(256), lds, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((dd_padded_kernel<T, F32>), grid, dim3(256), 0, st, a);
 }
 
 // O: output type of the gradients (F32, or T for 16-bit gradients).
@@ -1615,14 +1754,17 @@ int maxsim_amd_contrastive_backward(
       workspace_bytes, stream);
 }
 
-int maxsim_amd_padded_backward(
-    maxsim_dtype dtype, const float* dscore, const void* queries,
+int maxsim_amd_padded_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
     const void* documents, const int32_t* query_lengths,
     const int32_t* doc_lengths, const int32_t* argmax, int64_t batch,
     int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
-    float* dqueries, float* ddocuments, void* stream) {
+    void* dqueries, void* ddocuments, void* stream) {
   clear_error();
   if (int e = check_dtype(dtype)) return e;
+  if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
+    return fail(MAXSIM_ERR_INVALID, "grad_dtype must be FLOAT32 or the input dtype");
+  const bool out16 = grad_dtype != MAXSIM_FLOAT32;
   if (batch < 0 || num_candidates < 0) return fail(MAXSIM_ERR_INVALID, "negative size");
   if (Lq_max <= 0 || Ld_max <= 0)
     return fail(MAXSIM_ERR_INVALID, "Lq_max and Ld_max must be > 0");
@@ -1632,7 +1774,7 @@ int maxsim_amd_padded_backward(
   if (!dqueries || (num_candidates > 0 && !ddocuments))
     return fail(MAXSIM_ERR_INVALID, "null gradient pointer");
   if (num_candidates == 0) {
-    launch_fill(dqueries, batch * Lq_max * dim, st);
+    launch_fill_grad(dqueries, batch * Lq_max * dim, out16, st);
     return check_launch("fill_zero_kernel");
   }
   if (!dscore || !queries || !documents || !query_lengths || !doc_lengths || !argmax)
@@ -1656,7 +1798,7 @@ int maxsim_amd_padded_backward(
   qa.ncand = num_candidates;
   qa.ld_max = (int)Ld_max;
   qa.padded = 1;
-  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, false, st);
+  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
   if (int e = check_launch("dq_gather_kernel")) return e;
 
   PaddedDdArgs da{};
@@ -1671,8 +1813,36 @@ int maxsim_amd_padded_backward(
   da.lq_max = (int)Lq_max;
   da.ld_max = (int)Ld_max;
   da.dim = (int)dim;
-  MAXSIM_DISPATCH(dtype, launch_dd_padded, da, st);
+  da.pair = dim % 2 == 0 && reinterpret_cast<uintptr_t>(queries) % 4 == 0 &&
+            reinterpret_cast<uintptr_t>(ddocuments) % 4 == 0;
+  // Split each candidate's rows over several waves until the launch has
+  // about 16k waves (16 per SIMD), keeping at least 16 rows per wave.
+  {
+    const int64_t npairs = batch * num_candidates;
+    const int64_t by_waves = (16384 + npairs - 1) / npairs;
+    const int64_t by_rows = (Ld_max + 15) / 16;
+    const int64_t ns = std::max<int64_t>(1, std::min(by_waves, by_rows));
+    da.rows_per_split = (int)((Ld_max + ns - 1) / ns);
+    da.nsplit = (int)((Ld_max + da.rows_per_split - 1) / da.rows_per_split);
+    if ((npairs * da.nsplit + 3) / 4 > INT32_MAX)
+      return fail(MAXSIM_ERR_UNSUPPORTED, "too many candidates for one launch");
+  }
+  const int64_t am_rest = Lq_max - 64 * kDdAmRegs;
+  da.am_lds = out16 && am_rest > 0 && am_rest <= kDdAmLdsMax ? (int)am_rest : 0;
+  MAXSIM_DISPATCH(dtype, launch_dd_padded, da, out16, st);
   return check_launch("dd_padded_kernel");
+}
+
+int maxsim_amd_padded_backward(
+    maxsim_dtype dtype, const float* dscore, const void* queries,
+    const void* documents, const int32_t* query_lengths,
+    const int32_t* doc_lengths, const int32_t* argmax, int64_t batch,
+    int64_t num_candidates, int64_t Lq_max, int64_t Ld_max, int64_t dim,
+    float* dqueries, float* ddocuments, void* stream) {
+  return maxsim_amd_padded_backward_typed(dtype, MAXSIM_FLOAT32, dscore, queries, documents,
+                                          query_lengths, doc_lengths, argmax, batch,
+                                          num_candidates, Lq_max, Ld_max, dim, dqueries,
+                                          ddocuments, stream);
 }
 
 size_t maxsim_amd_packed_backward_workspace_size(int64_t num_queries, int64_t num_documents,

@@ -313,10 +313,12 @@ std::tuple<Tensor, Tensor> maxsim_padded_forward_with_argmax(
   return {scores, argmax};
 }
 
-std::tuple<Tensor, Tensor> maxsim_padded_backward(
+// grads_in_input_dtype: gradients written in the inputs' dtype by the typed
+// entry point (rounded to nearest even, the bits of a cast of the fp32 ones).
+std::tuple<Tensor, Tensor> padded_backward_impl(
     Tensor dscore, Tensor queries, Tensor documents, Tensor query_lengths,
     Tensor doc_lengths, Tensor argmax, int64_t Lq_max, int64_t Ld_max,
-    int64_t num_candidates) {
+    int64_t num_candidates, bool grads_in_input_dtype) {
   Padded p = prep_padded(queries, query_lengths, documents, doc_lengths, Lq_max,
                          Ld_max, num_candidates);
   TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
@@ -327,15 +329,34 @@ std::tuple<Tensor, Tensor> maxsim_padded_backward(
   TORCH_CHECK(dscore.numel() == p.B * p.C, "dscore must have B*C elements");
   Tensor g = dscore.contiguous();
   Tensor am = argmax.contiguous();
-  Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, f32_opts(p.q));
-  Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, f32_opts(p.q));
+  const maxsim_dtype dt = to_dtype(p.q);
+  const bool typed = grads_in_input_dtype && dt != MAXSIM_FLOAT32;
+  const at::TensorOptions opts = typed ? p.q.options() : f32_opts(p.q);
+  Tensor dq = at::empty({p.q.size(0), p.q.size(1)}, opts);
+  Tensor dd = at::empty({p.d.size(0), p.d.size(1)}, opts);
   c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
-  check_status(maxsim_amd_padded_backward(
-      to_dtype(p.q), g.data_ptr<float>(), p.q.data_ptr(), p.d.data_ptr(),
+  check_status(maxsim_amd_padded_backward_typed(
+      dt, typed ? dt : MAXSIM_FLOAT32, g.data_ptr<float>(), p.q.data_ptr(), p.d.data_ptr(),
       p.qlen.data_ptr<int32_t>(), p.dlen.data_ptr<int32_t>(), am.data_ptr<int32_t>(),
-      p.B, p.C, Lq_max, Ld_max, p.q.size(1), dq.data_ptr<float>(),
-      dd.data_ptr<float>(), current_stream(p.q)));
+      p.B, p.C, Lq_max, Ld_max, p.q.size(1), dq.data_ptr(), dd.data_ptr(),
+      current_stream(p.q)));
   return {dq, dd};
+}
+
+std::tuple<Tensor, Tensor> maxsim_padded_backward(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor query_lengths,
+    Tensor doc_lengths, Tensor argmax, int64_t Lq_max, int64_t Ld_max,
+    int64_t num_candidates) {
+  return padded_backward_impl(dscore, queries, documents, query_lengths, doc_lengths, argmax,
+                              Lq_max, Ld_max, num_candidates, false);
+}
+
+std::tuple<Tensor, Tensor> maxsim_padded_backward_typed(
+    Tensor dscore, Tensor queries, Tensor documents, Tensor query_lengths,
+    Tensor doc_lengths, Tensor argmax, int64_t Lq_max, int64_t Ld_max,
+    int64_t num_candidates) {
+  return padded_backward_impl(dscore, queries, documents, query_lengths, doc_lengths, argmax,
+                              Lq_max, Ld_max, num_candidates, true);
 }
 
 // ---- contrastive ----------------------------------------------------------
@@ -514,6 +535,9 @@ TORCH_LIBRARY(maxsim_amd, m) {
   m.def("maxsim_packed_backward_typed(Tensor dscore, Tensor queries, Tensor query_offsets, "
         "Tensor documents, Tensor document_offsets, Tensor pair_query_ids, "
         "Tensor pair_document_ids, Tensor argmax, int max_q_len) -> (Tensor, Tensor)");
+  m.def("maxsim_padded_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
+        "Tensor query_lengths, Tensor doc_lengths, Tensor argmax, int Lq_max, "
+        "int Ld_max, int num_candidates) -> (Tensor, Tensor)");
   m.def("maxsim_pack_padded_rows(Tensor padded, Tensor lengths, Tensor offsets, int max_len, "
         "int packed_rows) -> Tensor");
   m.def("maxsim_contrastive_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
@@ -525,6 +549,7 @@ TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
   m.impl("maxsim_padded_forward", &maxsim_padded_forward);
   m.impl("maxsim_padded_forward_with_argmax", &maxsim_padded_forward_with_argmax);
   m.impl("maxsim_padded_backward", &maxsim_padded_backward);
+  m.impl("maxsim_padded_backward_typed", &maxsim_padded_backward_typed);
   m.impl("maxsim_packed_forward_with_argmax", &maxsim_packed_forward_with_argmax);
   m.impl("maxsim_packed_backward", &maxsim_packed_backward);
   m.impl("maxsim_packed_backward_typed", &maxsim_packed_backward_typed);

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 16, names
+    assert len(names) == 17, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 6
+    assert lib.maxsim_amd_abi_version() == 7
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -182,6 +182,19 @@ def test_typed_packed_backward_16bit_needs_the_grouped_path(lib):
     assert b"fp32" in lib.maxsim_amd_last_error()
     # max_q_len beyond the 16-bit entry ids of the grouped kernels: refused too
     assert _typed_packed_backward(lib, mql=70000, ws=P(16), ws_bytes=1 << 20) == UNSUPPORTED
+
+
+def test_typed_padded_backward_rejects_a_third_grad_dtype(lib):
+    fn = lib.maxsim_amd_padded_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P,
+                   P]
+    one = P(16)
+    assert fn(BF16, F16, one, one, one, one, one, one, 2, 3, 8, 16, 64, one, one, None) == INVALID
+    assert b"grad_dtype" in lib.maxsim_amd_last_error()
+    assert fn(F16, F16, one, one, one, one, one, one, 2, 3, 8, 16, 300, one, one, None) != OK
+    # no queries: nothing to write, success without a launch
+    assert fn(BF16, BF16, None, None, None, None, None, None, 0, 3, 8, 16, 64, None, None,
+              None) == OK
 
 
 def test_pack_rejects_bad_arguments(lib):

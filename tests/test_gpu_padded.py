@@ -186,3 +186,122 @@ def test_padded_bad_device_lengths_raise_after_queueing(fn, which, value, patter
     s_ref, _ = oracle.padded_forward(np64(q), np64(d), npi(qlen), npi(dlen))
     assert_close(maxsim_amd.score_candidates_padded(q, d, qlen, dlen), s_ref,
                  **SCORE_TOL[torch.float16])
+
+
+# ---------------------------------------------------------------------------
+# gradients in the input dtype (the autograd path's operator)
+# ---------------------------------------------------------------------------
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+TYPED = [
+    # B, C, Lq, Ld, dim
+    pytest.param(3, 4, 32, 100, 64, id="basic"),
+    pytest.param(2, 3, 40, 33, 20, id="dim20-element-wise"),
+    pytest.param(2, 2, 48, 70, 256, id="dim256"),
+    pytest.param(2, 3, 200, 3, 32, id="three-rows-many-tokens-each"),
+    pytest.param(2, 2, 330, 40, 64, id="Lq330-argmax-in-lds"),
+    pytest.param(1, 2, 4400, 20, 16, id="Lq4400-argmax-from-global"),
+    pytest.param(2, 2, 30, 25, 7, id="dim7-odd-element-wise"),
+    pytest.param(1, 1, 1, 1, 16, id="smallest"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+@pytest.mark.parametrize("B,C,Lq,Ld,dim", TYPED)
+def test_padded_backward_typed_is_cast_fp32_bit_for_bit(B, C, Lq, Ld, dim, dtype):
+    """The typed operator sums each gradient element in the same fp32 order
+    as the fp32 one and rounds to nearest even, so it is the cast of the
+    fp32 gradients bit for bit (padding rows included), and close to the
+    oracle."""
+    # the first query uses all Lq tokens (past the 256 kept in registers when
+    # Lq > 256), the others about half, which leaves padding rows
+    qlen = [Lq] + [max(1, Lq // 2 + b) for b in range(1, B)]
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, dim, dtype, seed=B * Lq + dim, qlen=qlen)
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    g = torch.randn(B * C, generator=torch.Generator().manual_seed(Ld)).to(DEVICE)
+    qf, df = q.reshape(B * Lq, dim), d.reshape(B * C * Ld, dim)
+    args = (g, qf, df, qlen.to(torch.int32), dlen.reshape(-1).to(torch.int32),
+            am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
+    dq32, dd32 = ops.maxsim_padded_backward(*args)
+    dq, dd = ops.maxsim_padded_backward_typed(*args)
+    assert dq.dtype == dtype and dd.dtype == dtype
+    assert torch.equal(_bits(dq), _bits(dq32.to(dtype)))
+    assert torch.equal(_bits(dd), _bits(dd32.to(dtype)))
+    dq_ref, dd_ref = oracle.padded_backward(np64(g.view(B, C)), np64(q), np64(d), npi(qlen),
+                                            npi(dlen), npi(am))
+    assert_close(dq.view(B, Lq, dim), dq_ref, rtol=1e-2, atol=1e-2)
+    assert_close(dd.view(B, C, Ld, dim), dd_ref, rtol=1e-2, atol=1e-2)
+
+
+def test_padded_backward_typed_misaligned_views_match_fp32():
+    """16-bit views that start 2 bytes into their storage take the 16-bit
+    element path instead of 32-bit accesses; same bits as the cast."""
+    B, C, Lq, Ld, dim = 2, 3, 20, 30, 32
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, dim, torch.float16, seed=23)
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    qbuf = torch.empty(B * Lq * dim + 1, dtype=torch.float16, device=DEVICE)
+    qbuf[1:].copy_(q.reshape(-1))
+    qv = qbuf[1:].view(B * Lq, dim)
+    assert qv.data_ptr() % 4 == 2
+    g = torch.randn(B * C, generator=torch.Generator().manual_seed(8)).to(DEVICE)
+    args = (g, qv, d.reshape(B * C * Ld, dim), qlen, dlen.reshape(-1),
+            am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
+    dq32, dd32 = ops.maxsim_padded_backward(*args)
+    dq, dd = ops.maxsim_padded_backward_typed(*args)
+    assert torch.equal(_bits(dq), _bits(dq32.to(torch.float16)))
+    assert torch.equal(_bits(dd), _bits(dd32.to(torch.float16)))
+
+
+def test_padded_backward_typed_invalid_lengths_match_fp32():
+    """Lengths the operator does not validate (0, beyond the padding): the
+    typed gradients are still the cast of the fp32 ones, zero for the
+    invalid query and candidates."""
+    B, C, Lq, Ld, dim = 3, 3, 16, 24, 32
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, dim, torch.bfloat16, seed=41)
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    bq, bd = qlen.clone().to(torch.int32), dlen.clone().reshape(-1).to(torch.int32)
+    bq[2] = 0
+    bd[1] = 0
+    bd[4] = Ld + 5
+    g = torch.randn(B * C, generator=torch.Generator().manual_seed(3)).to(DEVICE)
+    args = (g, q.reshape(B * Lq, dim), d.reshape(B * C * Ld, dim), bq, bd,
+            am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
+    dq32, dd32 = ops.maxsim_padded_backward(*args)
+    dq, dd = ops.maxsim_padded_backward_typed(*args)
+    assert torch.equal(_bits(dq), _bits(dq32.to(torch.bfloat16)))
+    assert torch.equal(_bits(dd), _bits(dd32.to(torch.bfloat16)))
+    assert torch.all(dq.view(B, Lq, dim)[2] == 0)
+    assert torch.all(dd.view(B * C, Ld, dim)[[1, 4, 6, 7, 8]] == 0)
+
+
+def test_padded_backward_typed_fp32_inputs_are_fp32():
+    q, d, qlen, dlen = make_padded(2, 3, 16, 40, 32, torch.float32, seed=6)
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    g = torch.randn(6, generator=torch.Generator().manual_seed(1)).to(DEVICE)
+    args = (g, q.reshape(32, 32), d.reshape(240, 32), qlen.to(torch.int32),
+            dlen.reshape(-1).to(torch.int32), am.reshape(6, 16).contiguous(), 16, 40, 3)
+    dq, dd = ops.maxsim_padded_backward_typed(*args)
+    dq32, dd32 = ops.maxsim_padded_backward(*args)
+    assert dq.dtype == torch.float32 and dd.dtype == torch.float32
+    assert torch.equal(dq, dq32) and torch.equal(dd, dd32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+def test_padded_train_grads_in_input_dtype(dtype):
+    """score_candidates_padded_train: .grad has the input dtype and equals
+    the fp32 operator's gradient cast, bit for bit."""
+    B, C, Lq, Ld, D = 2, 4, 24, 60, 64
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, D, dtype, seed=19)
+    qg, dg = q.clone().requires_grad_(True), d.clone().requires_grad_(True)
+    w = torch.randn(B, C, generator=torch.Generator().manual_seed(5)).to(DEVICE)
+    (maxsim_amd.score_candidates_padded_train(qg, dg, qlen, dlen) * w).sum().backward()
+    assert qg.grad.dtype == dtype and dg.grad.dtype == dtype
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    dq32, dd32 = ops.maxsim_padded_backward(
+        w.reshape(-1).contiguous(), q.reshape(B * Lq, D), d.reshape(B * C * Ld, D),
+        qlen.to(torch.int32), dlen.reshape(-1).to(torch.int32),
+        am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
+    assert torch.equal(_bits(qg.grad.reshape(B * Lq, D)), _bits(dq32.to(dtype)))
+    assert torch.equal(_bits(dg.grad.reshape(B * C * Ld, D)), _bits(dd32.to(dtype)))
