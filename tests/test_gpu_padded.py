@@ -202,6 +202,7 @@ TYPED = [
     pytest.param(2, 2, 48, 70, 256, id="dim256"),
     pytest.param(2, 3, 200, 3, 32, id="three-rows-many-tokens-each"),
     pytest.param(2, 2, 330, 40, 64, id="Lq330-argmax-in-lds"),
+    pytest.param(1, 2, 4352, 20, 16, id="Lq4352-argmax-lds-at-its-64KB-cap"),
     pytest.param(1, 2, 4400, 20, 16, id="Lq4400-argmax-from-global"),
     pytest.param(2, 2, 30, 25, 7, id="dim7-odd-element-wise"),
     pytest.param(1, 1, 1, 1, 16, id="smallest"),
