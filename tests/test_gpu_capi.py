@@ -165,6 +165,42 @@ def test_packed_backward_typed_through_the_abi(lib):
     assert_close(dd, dd_ref, rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_padded_backward_typed_through_the_abi(lib, dtype):
+    """maxsim_amd_padded_backward_typed in the input dtype fills NaN-filled
+    buffers, padding rows included, with exactly the bits of
+    maxsim_amd_padded_backward's fp32 gradients cast to that dtype."""
+    from ._helpers import make_padded
+
+    B, C, Lq, Ld, D = 3, 5, 40, 90, 128
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, D, dtype, seed=27)
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    am = am.contiguous()
+    g = torch.randn(B * C, generator=torch.Generator().manual_seed(6)).to(DEVICE)
+    dl = dlen.reshape(-1).contiguous()
+    typed = lib.maxsim_amd_padded_backward_typed
+    typed.argtypes = [ctypes.c_int, ctypes.c_int, P, P, P, P, P, P, I64, I64, I64, I64, I64, P,
+                      P, P]
+    fp32 = lib.maxsim_amd_padded_backward
+    fp32.argtypes = [ctypes.c_int, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]
+    stream = torch.cuda.current_stream().cuda_stream
+    dq = torch.full((B * Lq, D), float("nan"), dtype=dtype, device=DEVICE)
+    dd = torch.full((B * C * Ld, D), float("nan"), dtype=dtype, device=DEVICE)
+    rc = typed(DT[dtype], DT[dtype], g.data_ptr(), q.data_ptr(), d.data_ptr(), qlen.data_ptr(),
+               dl.data_ptr(), am.data_ptr(), B, C, Lq, Ld, D, dq.data_ptr(), dd.data_ptr(),
+               stream)
+    assert rc == 0, lib.maxsim_amd_last_error()
+    dq32 = torch.full((B * Lq, D), float("nan"), device=DEVICE)
+    dd32 = torch.full((B * C * Ld, D), float("nan"), device=DEVICE)
+    rc = fp32(DT[dtype], g.data_ptr(), q.data_ptr(), d.data_ptr(), qlen.data_ptr(), dl.data_ptr(),
+              am.data_ptr(), B, C, Lq, Ld, D, dq32.data_ptr(), dd32.data_ptr(), stream)
+    assert rc == 0, lib.maxsim_amd_last_error()
+    torch.cuda.synchronize()
+    assert not torch.isnan(dq32).any() and not torch.isnan(dd32).any()
+    assert torch.equal(dq.view(torch.int16), dq32.to(dtype).view(torch.int16))
+    assert torch.equal(dd.view(torch.int16), dd32.to(dtype).view(torch.int16))
+
+
 def test_pack_padded_rows_through_the_abi(lib):
     """maxsim_amd_pack_padded_rows copies each segment's first rows to its
     offset, bit for bit, and leaves rows past the written ones untouched."""
