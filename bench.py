@@ -534,7 +534,33 @@ def main():
                             "gbps": round(bytes_pack / (ms_pack * 1e-3) / 1e9, 1),
                             "hbm_frac": round(bytes_pack / (ms_pack * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"C3 pack: {ms_pack:.3f} ms, {bytes_pack / (ms_pack * 1e-3) / 1e9:.0f} GB/s")
-        del q3, d3, qf, df
+        # padded training backward over the first 16 candidates of each C3
+        # query (not a BASELINE configuration): gradients written in fp16 by
+        # the autograd path's operator, against the fp32 operator plus the
+        # cast that autograd applies after the reference's backward
+        Ct = 16
+        dtf = d3[:, :Ct].contiguous().reshape(B * Ct * Ld, 128)
+        dltf = dl3[:, :Ct].contiguous().reshape(-1)
+        _, amt = ops.maxsim_padded_forward_with_argmax(qf, ql3, dtf, dltf, 32, Ld, Ct)
+        gt = torch.randn(B * Ct, generator=torch.Generator(device=dev).manual_seed(3), device=dev)
+        bargs = (gt, qf, dtf, ql3, dltf, amt, 32, Ld, Ct)
+
+        def cast_route():
+            dq_, dd_ = ops.maxsim_padded_backward(*bargs)
+            return dq_.half(), dd_.half()
+
+        ms_bt = time_events(torch, lambda: ops.maxsim_padded_backward_typed(*bargs), K, 2)
+        ms_bc = time_events(torch, cast_route, K, 2)
+        # fp16 dQ and dD (padding rows included) written; Q read once, one
+        # document row gathered per (candidate, token); argmax, dscore, lengths
+        bytes_bt = (2 * 128 * (B * 32 + B * Ct * Ld) + 2 * 128 * (B * 32 + B * Ct * 32)
+                    + 4 * (B * Ct * 32 + 2 * B * Ct + B))
+        extra["c3_train_bwd"] = {"candidates": f"{B}x{Ct}", "typed_ms": round(ms_bt, 4),
+                                 "fp32_plus_cast_ms": round(ms_bc, 4),
+                                 "typed_gbps": round(bytes_bt / (ms_bt * 1e-3) / 1e9, 1),
+                                 "typed_hbm_frac": round(bytes_bt / (ms_bt * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"C3 train bwd ({B}x{Ct}): typed {ms_bt:.3f} ms, fp32 + cast {ms_bc:.3f} ms")
+        del q3, d3, qf, df, dtf, amt
         torch.cuda.empty_cache()
 
         # ---------------- C4: packed pairs fwd + bwd ----------------
