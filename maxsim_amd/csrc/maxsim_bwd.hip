@@ -697,6 +697,7 @@ struct PaddedDdArgs {
   int am_lds;  // 16-bit O: argmax ints per wave staged in LDS (0: none)
   int nsplit;  // waves per candidate, each owning rows_per_split rows
   int rows_per_split;
+  int vec_rows;  // 16-bit O: 64 % (dim / 8) == 0, q and dd 16-byte aligned
 };
 
 // Element x of query row qrow as fp32.
@@ -815,6 +816,81 @@ __device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t 
   }
 }
 
+// 16-bit O with a.vec_rows: the same sums, with each lane owning 8 elements
+// (16 bytes) of one row, so a wave covers 64 / (dim / 8) rows per step and
+// writes them with one 16-byte store per lane.  For each token landing in the
+// step's rows (in token order) only the lanes of its row add it, so every
+// element sees the fmaf sequence of the fp32 kernel.
+template <typename T, typename O>
+__device__ __forceinline__ void dd_padded_rows16_vec(const PaddedDdArgs& a, int64_t p, int64_t b,
+                                                     int r0, int r1, int lane, int32_t* am_lds) {
+  using S = typename T::storage;
+  uint16_t* base = static_cast<uint16_t*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
+  const int lqb = a.qlen[b];
+  const int ld = a.dlen[p];
+  const bool ok = lqb >= 1 && lqb <= a.lq_max && ld >= 1 && ld <= a.ld_max;
+  const float g = a.dscore[p];
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const int32_t* am = a.argmax + p * a.lq_max;
+  int amv[kDdAmRegs];
+#pragma unroll
+  for (int c = 0; c < kDdAmRegs; ++c) {
+    const int t = 64 * c + lane;
+    amv[c] = ok && t < lqb ? am[t] : -1;
+  }
+  if (a.am_lds) {
+    if (ok)
+      for (int t = 64 * kDdAmRegs + lane; t < lqb; t += 64) am_lds[t - 64 * kDdAmRegs] = am[t];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  const int L = a.dim >> 3;  // lanes per row
+  const int rpi = 64 / L;    // rows per step
+  const int sub = lane / L;
+  const int e0 = (lane - sub * L) * 8;
+  const int rmax = min(r1, ld);  // rows that can receive tokens
+  for (int rb = r0; rb < r1; rb += rpi) {
+    const int r = rb + sub;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (ok && rb < rmax) {
+      const int rhi = min(rb + rpi, rmax);
+      for (int c0 = 0; c0 < lqb; c0 += 64) {
+        const int t = c0 + lane;
+        int j = -1;
+        if (c0 < 64 * kDdAmRegs) {
+#pragma unroll
+          for (int c = 0; c < kDdAmRegs; ++c)
+            if (c0 == 64 * c) j = amv[c];
+        } else if (t < lqb) {
+          j = a.am_lds ? am_lds[t - 64 * kDdAmRegs] : am[t];
+        }
+        uint64_t hits = __ballot(j >= rb && j < rhi);
+        while (hits) {
+          const int tl = __builtin_ctzll(hits);
+          hits &= hits - 1;
+          const int jt = __builtin_amdgcn_readlane(j, tl);
+          if (r == jt) {
+            const uint4 w = *reinterpret_cast<const uint4*>(
+                Q + (b * a.lq_max + c0 + tl) * (int64_t)a.dim + e0);
+            const S* v = reinterpret_cast<const S*>(&w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(g, elem_f32<T>(v, e), acc[e]);
+          }
+        }
+      }
+    }
+    if (r < r1) {
+      uint4 o;
+      o.x = (uint32_t)to_out16<O>(acc[0]) | ((uint32_t)to_out16<O>(acc[1]) << 16);
+      o.y = (uint32_t)to_out16<O>(acc[2]) | ((uint32_t)to_out16<O>(acc[3]) << 16);
+      o.z = (uint32_t)to_out16<O>(acc[4]) | ((uint32_t)to_out16<O>(acc[5]) << 16);
+      o.w = (uint32_t)to_out16<O>(acc[6]) | ((uint32_t)to_out16<O>(acc[7]) << 16);
+      *reinterpret_cast<uint4*>(base + (int64_t)r * a.dim + e0) = o;
+    }
+  }
+}
+
 template <typename T, typename O>
 __global__ __launch_bounds__(256) void dd_padded_kernel(PaddedDdArgs a) {
   using S = typename T::storage;
@@ -829,7 +905,10 @@ __global__ __launch_bounds__(256) void dd_padded_kernel(PaddedDdArgs a) {
   if (r0 >= r1) return;
   if constexpr (O::bytes != 4) {
     extern __shared__ int32_t dd_am_lds[];
-    dd_padded_rows16<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
+    if (a.vec_rows)
+      dd_padded_rows16_vec<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
+    else
+      dd_padded_rows16<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
     return;
   }
   float* base = static_cast<float*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
@@ -1827,6 +1906,8 @@ int maxsim_amd_padded_backward_typed(
     if ((npairs * da.nsplit + 3) / 4 > INT32_MAX)
       return fail(MAXSIM_ERR_UNSUPPORTED, "too many candidates for one launch");
   }
+  da.vec_rows = dim % 8 == 0 && 64 % (dim / 8) == 0 && aligned16b(queries) &&
+                aligned16b(ddocuments);
   const int64_t am_rest = Lq_max - 64 * kDdAmRegs;
   da.am_lds = out16 && am_rest > 0 && am_rest <= kDdAmLdsMax ? (int)am_rest : 0;
   MAXSIM_DISPATCH(dtype, launch_dd_padded, da, out16, st);

@@ -200,6 +200,8 @@ TYPED = [
     pytest.param(3, 4, 32, 100, 64, id="basic"),
     pytest.param(2, 3, 40, 33, 20, id="dim20-element-wise"),
     pytest.param(2, 2, 48, 70, 256, id="dim256"),
+    pytest.param(2, 3, 50, 70, 8, id="dim8-one-lane-per-row"),
+    pytest.param(2, 2, 24, 40, 96, id="dim96-element-pairs"),
     pytest.param(2, 3, 200, 3, 32, id="three-rows-many-tokens-each"),
     pytest.param(2, 2, 330, 40, 64, id="Lq330-argmax-in-lds"),
     pytest.param(1, 2, 4352, 20, 16, id="Lq4352-argmax-lds-at-its-64KB-cap"),
