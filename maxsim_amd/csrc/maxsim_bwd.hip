@@ -694,10 +694,10 @@ struct PaddedDdArgs {
   int ld_max;
   int dim;
   int pair;    // 16-bit O: dim even, q and dd 4-byte aligned (32-bit accesses)
-  int am_lds;  // 16-bit O: argmax ints per wave staged in LDS (0: none)
+  int am_lds;  // argmax ints per wave staged in LDS (0: none)
   int nsplit;  // waves per candidate, each owning rows_per_split rows
   int rows_per_split;
-  int vec_rows;  // 16-bit O: 64 % (dim / 8) == 0, q and dd 16-byte aligned
+  int vec_rows;  // 64 % (dim / 8) == 0, q and dd 16-byte aligned: whole rows per lane group
 };
 
 // Element x of query row qrow as fp32.
@@ -816,16 +816,16 @@ __device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t 
   }
 }
 
-// 16-bit O with a.vec_rows: the same sums, with each lane owning 8 elements
-// (16 bytes) of one row, so a wave covers 64 / (dim / 8) rows per step and
-// writes them with one 16-byte store per lane.  For each token landing in the
-// step's rows (in token order) only the lanes of its row add it, so every
-// element sees the fmaf sequence of the fp32 kernel.
+// a.vec_rows (either output type): each lane owns 8 elements of one row, so
+// a wave covers 64 / (dim / 8) rows per step and writes each row once (16
+// bytes per lane for 16-bit O, 32 for fp32), zeros included.  For each token
+// landing in the step's rows (in token order) only the lanes of its row add
+// it, so every element sees the fmaf sequence of the scalar fp32 path below.
 template <typename T, typename O>
-__device__ __forceinline__ void dd_padded_rows16_vec(const PaddedDdArgs& a, int64_t p, int64_t b,
-                                                     int r0, int r1, int lane, int32_t* am_lds) {
+__device__ __forceinline__ void dd_padded_rows_vec(const PaddedDdArgs& a, int64_t p, int64_t b,
+                                                   int r0, int r1, int lane, int32_t* am_lds) {
   using S = typename T::storage;
-  uint16_t* base = static_cast<uint16_t*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
+  const int64_t base = p * a.ld_max * (int64_t)a.dim;
   const int lqb = a.qlen[b];
   const int ld = a.dlen[p];
   const bool ok = lqb >= 1 && lqb <= a.lq_max && ld >= 1 && ld <= a.ld_max;
@@ -871,22 +871,39 @@ __device__ __forceinline__ void dd_padded_rows16_vec(const PaddedDdArgs& a, int6
           hits &= hits - 1;
           const int jt = __builtin_amdgcn_readlane(j, tl);
           if (r == jt) {
-            const uint4 w = *reinterpret_cast<const uint4*>(
-                Q + (b * a.lq_max + c0 + tl) * (int64_t)a.dim + e0);
-            const S* v = reinterpret_cast<const S*>(&w);
+            const S* src = Q + (b * a.lq_max + c0 + tl) * (int64_t)a.dim + e0;
+            float qv[8];
+            if constexpr (T::bytes == 4) {
+              const float4 w0 = reinterpret_cast<const float4*>(src)[0];
+              const float4 w1 = reinterpret_cast<const float4*>(src)[1];
+              qv[0] = w0.x; qv[1] = w0.y; qv[2] = w0.z; qv[3] = w0.w;
+              qv[4] = w1.x; qv[5] = w1.y; qv[6] = w1.z; qv[7] = w1.w;
+            } else {
+              const uint4 w = *reinterpret_cast<const uint4*>(src);
+              const S* v = reinterpret_cast<const S*>(&w);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(g, elem_f32<T>(v, e), acc[e]);
+              for (int e = 0; e < 8; ++e) qv[e] = elem_f32<T>(v, e);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(g, qv[e], acc[e]);
           }
         }
       }
     }
     if (r < r1) {
-      uint4 o;
-      o.x = (uint32_t)to_out16<O>(acc[0]) | ((uint32_t)to_out16<O>(acc[1]) << 16);
-      o.y = (uint32_t)to_out16<O>(acc[2]) | ((uint32_t)to_out16<O>(acc[3]) << 16);
-      o.z = (uint32_t)to_out16<O>(acc[4]) | ((uint32_t)to_out16<O>(acc[5]) << 16);
-      o.w = (uint32_t)to_out16<O>(acc[6]) | ((uint32_t)to_out16<O>(acc[7]) << 16);
-      *reinterpret_cast<uint4*>(base + (int64_t)r * a.dim + e0) = o;
+      const int64_t at = base + (int64_t)r * a.dim + e0;
+      if constexpr (O::bytes == 4) {
+        float4* dst = reinterpret_cast<float4*>(static_cast<float*>(a.dd) + at);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      } else {
+        uint4 o;
+        o.x = (uint32_t)to_out16<O>(acc[0]) | ((uint32_t)to_out16<O>(acc[1]) << 16);
+        o.y = (uint32_t)to_out16<O>(acc[2]) | ((uint32_t)to_out16<O>(acc[3]) << 16);
+        o.z = (uint32_t)to_out16<O>(acc[4]) | ((uint32_t)to_out16<O>(acc[5]) << 16);
+        o.w = (uint32_t)to_out16<O>(acc[6]) | ((uint32_t)to_out16<O>(acc[7]) << 16);
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.dd) + at) = o;
+      }
     }
   }
 }
@@ -903,12 +920,14 @@ __global__ __launch_bounds__(256) void dd_padded_kernel(PaddedDdArgs a) {
   const int r0 = (int)(w - p * a.nsplit) * a.rows_per_split;
   const int r1 = min(a.ld_max, r0 + a.rows_per_split);
   if (r0 >= r1) return;
+  extern __shared__ int32_t dd_am_lds[];
+  int32_t* am_lds = dd_am_lds + (threadIdx.x >> 6) * a.am_lds;
+  if (a.vec_rows) {
+    dd_padded_rows_vec<T, O>(a, p, b, r0, r1, lane, am_lds);
+    return;
+  }
   if constexpr (O::bytes != 4) {
-    extern __shared__ int32_t dd_am_lds[];
-    if (a.vec_rows)
-      dd_padded_rows16_vec<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
-    else
-      dd_padded_rows16<T, O>(a, p, b, r0, r1, lane, dd_am_lds + (threadIdx.x >> 6) * a.am_lds);
+    dd_padded_rows16<T, O>(a, p, b, r0, r1, lane, am_lds);
     return;
   }
   float* base = static_cast<float*>(a.dd) + p * a.ld_max * (int64_t)a.dim;
@@ -1615,7 +1634,9 @@ static void launch_dd_padded(const PaddedDdArgs& a, bool out16, hipStream_t st) 
       return;
     }
   }
-  hipLaunchKernelGGL((dd_padded_kernel<T, F32>), grid, dim3(256), 0, st, a);
+  // the fp32 output takes the argmax LDS only on the vec_rows path
+  const size_t lds = a.vec_rows ? (size_t)4 * a.am_lds * sizeof(int32_t) : 0;
+  hipLaunchKernelGGL((dd_padded_kernel<T, F32>), grid, dim3(256), lds, st, a);
 }
 
 // O: output type of the gradients (F32, or T for 16-bit gradients).
@@ -1909,7 +1930,7 @@ int maxsim_amd_padded_backward_typed(
   da.vec_rows = dim % 8 == 0 && 64 % (dim / 8) == 0 && aligned16b(queries) &&
                 aligned16b(ddocuments);
   const int64_t am_rest = Lq_max - 64 * kDdAmRegs;
-  da.am_lds = out16 && am_rest > 0 && am_rest <= kDdAmLdsMax ? (int)am_rest : 0;
+  da.am_lds = (out16 || da.vec_rows) && am_rest > 0 && am_rest <= kDdAmLdsMax ? (int)am_rest : 0;
   MAXSIM_DISPATCH(dtype, launch_dd_padded, da, out16, st);
   return check_launch("dd_padded_kernel");
 }
