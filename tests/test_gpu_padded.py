@@ -308,3 +308,28 @@ def test_padded_train_grads_in_input_dtype(dtype):
         am.reshape(B * C, Lq).contiguous(), Lq, Ld, C)
     assert torch.equal(_bits(qg.grad.reshape(B * Lq, D)), _bits(dq32.to(dtype)))
     assert torch.equal(_bits(dg.grad.reshape(B * C * Ld, D)), _bits(dd32.to(dtype)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("Lq,dim", [(40, 128), (300, 64), (24, 8)], ids=["Lq40-dim128", "Lq300-dim64",
+                                                                       "Lq24-dim8"])
+def test_padded_backward_row_paths_agree_bit_for_bit(Lq, dim, dtype):
+    """16-byte-aligned queries with dim/8 dividing 64 take the path that
+    writes each dD row once from its in-order sum; a view 2 or 4 bytes into
+    its storage takes the zero-then-add path.  Both operators (fp32 and typed
+    gradients) give the same bits on either path."""
+    B, C, Ld = 2, 3, 50
+    q, d, qlen, dlen = make_padded(B, C, Lq, Ld, dim, dtype, seed=Lq + dim, qlen=[Lq, Lq // 2])
+    _, am = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    qbuf = torch.empty(B * Lq * dim + 1, dtype=dtype, device=DEVICE)
+    qbuf[1:].copy_(q.reshape(-1))
+    q_off = qbuf[1:].view(B * Lq, dim)
+    assert q_off.data_ptr() % 16 != 0
+    g = torch.randn(B * C, generator=torch.Generator().manual_seed(2)).to(DEVICE)
+    rest = (d.reshape(B * C * Ld, dim), qlen, dlen.reshape(-1), am.reshape(B * C, Lq).contiguous(),
+            Lq, Ld, C)
+    for op in (ops.maxsim_padded_backward, ops.maxsim_padded_backward_typed):
+        dq_a, dd_a = op(g, q.reshape(B * Lq, dim), *rest)
+        dq_b, dd_b = op(g, q_off, *rest)
+        assert torch.equal(_bits(dq_a), _bits(dq_b))
+        assert torch.equal(_bits(dd_a), _bits(dd_b))
