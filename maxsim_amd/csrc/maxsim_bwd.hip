@@ -183,12 +183,18 @@ struct DqArgs {
   int64_t ncand;
   int ld_max;
   int padded;
+  int csplit = 1;  // padded: lanes sharing one (row, slice), each over a candidate range
 };
 
 template <typename T, typename O>
 __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
   using S = typename T::storage;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // padded with csplit > 1: csplit adjacent lanes (a power of two) share one
+  // (row, slice); lane cs walks candidates [cs * per, (cs + 1) * per) and the
+  // partial sums are added in cs order before the first lane stores
+  const int64_t gid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cs = (int)(gid0 & (a.csplit - 1));
+  const int64_t gid = gid0 / a.csplit;
   const int64_t row = gid / a.nslices;
   if (row >= a.rows) return;
   const int sl = (int)(gid - row * a.nslices);
@@ -237,8 +243,11 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
     }
   } else {
     const int lqb = a.qlen[qidx];
+    const int64_t per = (a.ncand + a.csplit - 1) / a.csplit;
+    const int64_t c_lo = cs * per;
+    const int64_t c_hi = min(a.ncand, c_lo + per);
     if (i < lqb && lqb <= a.lq) {
-      for (int64_t c0 = 0; c0 < a.ncand; c0 += U) {
+      for (int64_t c0 = c_lo; c0 < c_hi; c0 += U) {
         int64_t src[U];
         float w[U];
 #pragma unroll
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
           const int64_t c = c0 + u;
           src[u] = 0;
           w[u] = 0.0f;
-          if (c < a.ncand) {
+          if (c < c_hi) {
             const int64_t p = qidx * a.ncand + c;
             const int ld = a.dlen[p];
             const int j = a.argmax[p * a.lq + i];
@@ -269,6 +278,20 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
             acc[e2] = (w[u] != 0.0f) ? fmaf(gb, v[u][e2], acc[e2]) : acc[e2];
         }
       }
+    }
+    if (a.csplit > 1) {
+      // every lane of a group is live here (a group shares its row)
+      const int lead = (threadIdx.x & 63) & ~(a.csplit - 1);
+      float tot[8];
+#pragma unroll
+      for (int e2 = 0; e2 < 8; ++e2) tot[e2] = acc[e2];
+      for (int k = 1; k < a.csplit; ++k) {
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) tot[e2] += __shfl(acc[e2], lead + k, 64);
+      }
+      if (cs != 0) return;
+#pragma unroll
+      for (int e2 = 0; e2 < 8; ++e2) acc[e2] = tot[e2];
     }
   }
   store8<O>(out_at<O>(a.dq, row * a.dim), k0, a.dim, vec, acc);
@@ -1545,7 +1568,7 @@ static void launch_fill_grad(void* p, int64_t n, bool out16, hipStream_t st) {
 // out16: gradients in the input's 16-bit type T instead of fp32.
 template <typename T>
 static void launch_dq(const DqArgs& a, bool vec, bool out16, hipStream_t st) {
-  const int64_t threads = a.rows * a.nslices;
+  const int64_t threads = a.rows * a.nslices * a.csplit;
   const dim3 grid((unsigned)((threads + 255) / 256));
   if (out16)
     hipLaunchKernelGGL((dq_gather_kernel<T, T>), grid, dim3(256), 0, st, a, vec);
@@ -1898,6 +1921,12 @@ int maxsim_amd_padded_backward_typed(
   qa.ncand = num_candidates;
   qa.ld_max = (int)Ld_max;
   qa.padded = 1;
+  // split each row's candidates over up to 8 lanes until ~128k threads run
+  // (keeping at least 8 candidates per lane)
+  qa.csplit = 1;
+  while (qa.csplit < 8 && qa.rows * nslices * qa.csplit < 131072 &&
+         num_candidates >= 16 * qa.csplit)
+    qa.csplit *= 2;
   MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
   if (int e = check_launch("dq_gather_kernel")) return e;
 

@@ -29,6 +29,7 @@ SHAPES = [
     pytest.param(3, 4, 64, 50, 128, False, id="Lq64"),
     pytest.param(2, 3, 130, 40, 32, False, id="Lq130-three-block-groups"),
     pytest.param(2, 2, 32, 300, 128, False, id="Ld300"),
+    pytest.param(2, 37, 16, 40, 64, False, id="C37-dq-candidates-over-4-lanes"),
 ]
 
 
@@ -202,6 +203,7 @@ TYPED = [
     pytest.param(2, 2, 48, 70, 256, id="dim256"),
     pytest.param(2, 3, 50, 70, 8, id="dim8-one-lane-per-row"),
     pytest.param(2, 2, 24, 40, 96, id="dim96-element-pairs"),
+    pytest.param(2, 37, 24, 30, 64, id="C37-dq-candidates-over-4-lanes"),
     pytest.param(2, 3, 200, 3, 32, id="three-rows-many-tokens-each"),
     pytest.param(2, 2, 330, 40, 64, id="Lq330-argmax-in-lds"),
     pytest.param(1, 2, 4352, 20, 16, id="Lq4352-argmax-lds-at-its-64KB-cap"),
