@@ -1735,6 +1735,9 @@ static void launch_packed_bwd(const PackedBwdArgs& a, bool vec, hipStream_t st) 
     }                                                          \
   } while (0)
 
+// Largest grid of 256-thread workgroups in one dimension (2^32 - 1 work-items).
+constexpr int64_t kMaxBlocks256 = (int64_t)UINT32_MAX / 256;
+
 static int element_bytes(maxsim_dtype dt) { return dt == MAXSIM_FLOAT32 ? 4 : 2; }
 
 }  // namespace maxsim
@@ -1927,8 +1930,6 @@ int maxsim_amd_padded_backward_typed(
   while (qa.csplit < 8 && qa.rows * nslices * qa.csplit < 131072 &&
          num_candidates >= 16 * qa.csplit)
     qa.csplit *= 2;
-  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
-  if (int e = check_launch("dq_gather_kernel")) return e;
 
   PaddedDdArgs da{};
   da.dscore = dscore;
@@ -1953,13 +1954,18 @@ int maxsim_amd_padded_backward_typed(
     const int64_t ns = std::max<int64_t>(1, std::min(by_waves, by_rows));
     da.rows_per_split = (int)((Ld_max + ns - 1) / ns);
     da.nsplit = (int)((Ld_max + da.rows_per_split - 1) / da.rows_per_split);
-    if ((npairs * da.nsplit + 3) / 4 > INT32_MAX)
-      return fail(MAXSIM_ERR_UNSUPPORTED, "too many candidates for one launch");
   }
+  // Both grids are checked before anything is queued: a dispatch holds at
+  // most 2^32 - 1 work-items per dimension.
+  if ((batch * num_candidates * da.nsplit + 3) / 4 > kMaxBlocks256 ||
+      (qa.rows * nslices * qa.csplit + 255) / 256 > kMaxBlocks256)
+    return fail(MAXSIM_ERR_UNSUPPORTED, "too many candidates for one launch");
   da.vec_rows = dim % 8 == 0 && 64 % (dim / 8) == 0 && aligned16b(queries) &&
                 aligned16b(ddocuments);
   const int64_t am_rest = Lq_max - 64 * kDdAmRegs;
   da.am_lds = (out16 || da.vec_rows) && am_rest > 0 && am_rest <= kDdAmLdsMax ? (int)am_rest : 0;
+  MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
+  if (int e = check_launch("dq_gather_kernel")) return e;
   MAXSIM_DISPATCH(dtype, launch_dd_padded, da, out16, st);
   return check_launch("dd_padded_kernel");
 }

@@ -312,19 +312,24 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // One wave instruction moving 16 bytes per lane from global memory
 // (uniform base + per-lane 32-bit byte offset) straight into LDS at
-// m0 + 16 * lane.
+// m0 + 16 * lane.  m0 is an input operand of the asm ("{m0}"), so the
+// compiler itself writes it just before the instruction and knows it is
+// read; nothing reserved is clobbered behind its back.  The compiler's
+// hazard recognizer does not look inside inline asm, so the asm opens with
+// s_nop 4: five wait states cover both a VALU write (readfirstlane) of the
+// base SGPRs, which a VMEM read needs five states after, and the compiler's
+// SALU write of m0, which an LDS DMA needs one state after.
+// (__builtin_amdgcn_global_load_lds would need no asm, but then the
+// compiler puts an s_waitcnt vmcnt(0) before every LDS read that follows a
+// DMA, since it cannot tell the ring buffers apart, which serialises the
+// ring.)
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
-  // s_nop 4: the compiler does not check hazards inside inline asm; five
-  // wait states cover a VALU write (e.g. readfirstlane) of an SGPR this
-  // load reads as its base.  s_nop 0 after the m0 write covers M0 -> LDS DMA.
   __asm__ __volatile__(
       "s_nop 4\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1"
       :
-      : "v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(m0))
-      : "memory", "m0");
+      : "v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(m0))
+      : "memory");
 }
 
 template <typename T, int KS>
@@ -1056,8 +1061,14 @@ int maxsim_amd_packed_forward_with_argmax(
   if (!queries || !documents || !query_offsets || !document_offsets ||
       !pair_query_ids || !pair_document_ids || !scores)
     return fail(MAXSIM_ERR_INVALID, "null pointer argument");
-  if (max_q_len > (1 << 20))
+  // max_q_len sizes the argmax rows; without argmax it only bounds the
+  // segment lengths, and any bound >= the number of query rows is the same
+  // bound, so it is clamped instead of rejected.
+  if (argmax && max_q_len > (1 << 20))
     return fail(MAXSIM_ERR_UNSUPPORTED, "max_q_len too large");
+  if (!argmax) max_q_len = std::min<int64_t>(max_q_len, std::max<int64_t>(total_q_tokens, 1));
+  if (max_q_len > INT32_MAX)
+    return fail(MAXSIM_ERR_UNSUPPORTED, "more than 2^31 - 1 query rows");
   FwdArgs a{};
   a.q = queries;
   a.d = documents;
