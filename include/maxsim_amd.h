@@ -8,7 +8,10 @@
  * Every entry point:
  *   - takes raw DEVICE pointers, int64 sizes, a dtype tag and a HIP stream
  *     (pass a hipStream_t cast to void*; NULL = the null stream);
- *   - never allocates or frees memory and keeps no state between calls;
+ *   - never allocates or frees memory; the only state kept between calls is
+ *     per device and read-only to callers: cached device attributes (CU
+ *     count, LDS limit, raised kernel LDS limits) and the address of the
+ *     scratch array of maxsim_amd_packed_backward_typed_noalloc;
  *   - is asynchronous on `stream` (no host synchronisation);
  *   - returns MAXSIM_OK or an error code; maxsim_amd_last_error() then gives
  *     a message (thread-local, valid until the next call on that thread).
@@ -135,6 +138,27 @@ int maxsim_amd_packed_backward_typed(
     int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
     void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream);
+
+/* maxsim_amd_packed_backward_typed without a workspace argument and without
+ * any allocation: the pair grouping lists live in a file-scope device array
+ * of the library (16 MiB per device, held until the process ends), so the
+ * call allocates nothing and its kernels take that array's address.
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Limit: 2 * num_queries +
+ * 2 * num_documents + 2 * num_pairs + 2 <= 4,194,304 (else
+ * MAXSIM_ERR_UNSUPPORTED before anything is launched).  Every call on one
+ * device shares that device's array: calls that overlap on one device (two
+ * streams, two threads) race, so serialise them.  Same results as
+ * maxsim_amd_packed_backward_typed with a workspace. */
+int maxsim_amd_packed_backward_typed_noalloc(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    void* dqueries, void* ddocuments, void* stream);
 
 /* ---- Padded rerank ------------------------------------------------------ */
 

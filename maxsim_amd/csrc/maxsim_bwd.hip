@@ -29,6 +29,7 @@
 #include "maxsim_host.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace maxsim {
@@ -1740,6 +1741,150 @@ constexpr int64_t kMaxBlocks256 = (int64_t)UINT32_MAX / 256;
 
 static int element_bytes(maxsim_dtype dt) { return dt == MAXSIM_FLOAT32 ? 4 : 2; }
 
+// Bytes of the packed backward's grouping workspace: int32 qstart[nq + 1],
+// qcur[nq], dstart[nd + 1], dcur[nd], qlist[P], dlist[P].
+static size_t packed_workspace_bytes(int64_t nq, int64_t nd, int64_t np) {
+  if (nq < 0 || nd < 0 || np < 0) return 0;
+  const int64_t ints = 2 * nq + 1 + 2 * nd + 1 + 2 * np;
+  return (size_t)ints * sizeof(int32_t);
+}
+
+// ---------------------------------------------------------------------------
+// Device scratch for maxsim_amd_packed_backward_typed_noalloc: the grouping
+// workspace of the packed backward in a file-scope array, for callers that
+// cannot allocate (graph capture, serving loops).  Each device holds its own
+// copy for the life of the process.  In host code `scratch` names a host-side
+// stand-in, never the device memory: the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current,
+// and only that address is passed to kernels.  Every call on a device shares
+// that device's array, so calls that overlap on one device race; each call
+// clears the parts that must start at zero (the group counters) itself.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchInts = (size_t)4 << 20;  // 16 MiB
+constexpr size_t kScratchBytes = kScratchInts * sizeof(int32_t);
+static __device__ __align__(256) int32_t scratch[kScratchInts];
+
+constexpr int kMaxScratchDevices = 64;
+
+static int device_scratch(void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) return fail(MAXSIM_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(ge));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(MAXSIM_ERR_UNSUPPORTED, "device index %d beyond the %d this library tracks", dev,
+                kMaxScratchDevices);
+  static std::mutex mu;
+  static void* ptrs[kMaxScratchDevices] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MAXSIM_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return MAXSIM_OK;
+}
+
+static int packed_backward_impl(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (int e = check_dtype(dtype)) return e;
+  if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
+    return fail(MAXSIM_ERR_INVALID, "grad_dtype must be FLOAT32 or the input dtype");
+  const bool out16 = grad_dtype != MAXSIM_FLOAT32;
+  if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
+      num_documents < 0 || num_pairs < 0)
+    return fail(MAXSIM_ERR_INVALID, "negative size");
+  if (max_q_len <= 0)
+    return fail(MAXSIM_ERR_INVALID, "max_q_len must be > 0; got %lld", (long long)max_q_len);
+  if (int e = check_dim(dim)) return e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((total_q_tokens > 0 && !dqueries) || (total_d_tokens > 0 && !ddocuments))
+    return fail(MAXSIM_ERR_INVALID, "null gradient pointer");
+  const size_t ws_need =
+      packed_workspace_bytes(num_queries, num_documents, num_pairs);
+  const bool grouped = num_pairs > 0 && workspace && workspace_bytes >= ws_need &&
+                       max_q_len < (1 << 16) && num_pairs < INT32_MAX;
+  // 16-bit gradients are written once per row, which only the grouped
+  // kernels do (the atomic path adds into fp32 rows)
+  if (out16 && num_pairs > 0 && !grouped)
+    return fail(MAXSIM_ERR_UNSUPPORTED,
+                "16-bit gradients need the workspace and max_q_len < 65536; use fp32 gradients");
+  if (!grouped) {
+    if (total_q_tokens > 0) launch_fill_grad(dqueries, total_q_tokens * dim, out16, st);
+    if (total_d_tokens > 0) launch_fill_grad(ddocuments, total_d_tokens * dim, out16, st);
+    if (int e = check_launch("fill_zero_kernel")) return e;
+  }
+  if (num_pairs == 0) return MAXSIM_OK;
+  if (!dscore || !queries || !documents || !query_offsets || !document_offsets ||
+      !pair_query_ids || !pair_document_ids || !argmax)
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  const int nslices = (int)((dim + 7) / 8);
+  const int eb = element_bytes(dtype);
+  const bool vec = (dim % 8 == 0) && aligned16b(queries) && aligned16b(documents) &&
+                   ((dim * eb) % 16 == 0);
+  PackedBwdArgs a{};
+  a.dscore = dscore;
+  a.q = queries;
+  a.d = documents;
+  a.qoff = query_offsets;
+  a.doff = document_offsets;
+  a.qids = pair_query_ids;
+  a.dids = pair_document_ids;
+  a.argmax = argmax;
+  a.dq = dqueries;
+  a.dd = ddocuments;
+  a.nq = num_queries;
+  a.nd = num_documents;
+  a.total_q = total_q_tokens;
+  a.total_d = total_d_tokens;
+  a.npairs = num_pairs;
+  a.slots = (int)max_q_len;
+  a.dim = (int)dim;
+  a.nslices = nslices;
+  a.lanes_per_tok = pow2_at_least(nslices < 64 ? nslices : 64);
+  if (!grouped) {
+    MAXSIM_DISPATCH(dtype, launch_packed_bwd, a, vec, st);
+    return check_launch("packed_bwd_kernel");
+  }
+  // group the pairs by query and by document (counting sort in the workspace)
+  int32_t* w = static_cast<int32_t*>(workspace);
+  PackedGroups g{};
+  g.qstart = w;
+  g.qcur = g.qstart + (num_queries + 1);
+  g.dstart = g.qcur + num_queries;
+  g.dcur = g.dstart + (num_documents + 1);
+  g.qlist = g.dcur + num_documents;
+  g.dlist = g.qlist + num_pairs;
+  // zero qstart..dstart (qcur is written by the scan); fill works on the bits
+  launch_fill(reinterpret_cast<float*>(g.qstart),
+              (num_queries + 1) + num_queries + (num_documents + 1), st);
+  const int64_t pb = std::min<int64_t>((num_pairs + 255) / 256, 2048);
+  hipLaunchKernelGGL(pair_count_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
+  hipLaunchKernelGGL(group_scan_kernel, dim3(2), dim3(kScanThreads), 0, st, g, num_queries,
+                     num_documents);
+  hipLaunchKernelGGL(pair_scatter_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
+  if (int e = check_launch("pair grouping kernels")) return e;
+  if (total_q_tokens > 0)
+    launch_zero_outside(dqueries, out16, query_offsets, num_queries, total_q_tokens, dim, st);
+  if (total_d_tokens > 0)
+    launch_zero_outside(ddocuments, out16, document_offsets, num_documents, total_d_tokens, dim,
+                        st);
+  const int G = pow2_at_least(nslices < 16 ? nslices : 16);  // lanes per dd row
+  const bool vec_g = vec && aligned16b(dqueries) && aligned16b(ddocuments);
+  MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, out16, st);
+  return check_launch("dq_packed_kernel / dd_packed_kernel");
+}
+
 }  // namespace maxsim
 
 using namespace maxsim;
@@ -1984,9 +2129,7 @@ int maxsim_amd_padded_backward(
 
 size_t maxsim_amd_packed_backward_workspace_size(int64_t num_queries, int64_t num_documents,
                                                  int64_t num_pairs) {
-  if (num_queries < 0 || num_documents < 0 || num_pairs < 0) return 0;
-  const int64_t ints = 2 * num_queries + 1 + 2 * num_documents + 1 + 2 * num_pairs;
-  return (size_t)ints * sizeof(int32_t);
+  return packed_workspace_bytes(num_queries, num_documents, num_pairs);
 }
 
 int maxsim_amd_packed_backward_typed(
@@ -1999,92 +2142,55 @@ int maxsim_amd_packed_backward_typed(
     void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
     void* stream) {
   clear_error();
+  return packed_backward_impl(dtype, grad_dtype, dscore, queries, total_q_tokens, query_offsets,
+                              num_queries, documents, total_d_tokens, document_offsets,
+                              num_documents, pair_query_ids, pair_document_ids, num_pairs, argmax,
+                              max_q_len, dim, dqueries, ddocuments, workspace, workspace_bytes,
+                              stream);
+}
+
+int maxsim_amd_packed_backward_typed_noalloc(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t total_q_tokens, const int32_t* query_offsets, int64_t num_queries,
+    const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* pair_query_ids, const int32_t* pair_document_ids,
+    int64_t num_pairs, const int32_t* argmax, int64_t max_q_len, int64_t dim,
+    void* dqueries, void* ddocuments, void* stream) {
+  clear_error();
+  if (num_queries < 0 || num_documents < 0 || num_pairs < 0)
+    return fail(MAXSIM_ERR_INVALID, "negative size");
+  const size_t need = packed_workspace_bytes(num_queries, num_documents, num_pairs);
+  if (need > kScratchBytes)
+    return fail(MAXSIM_ERR_UNSUPPORTED,
+                "the grouping lists need %zu bytes; the no-allocation entry point holds %zu "
+                "(2 * num_queries + 2 * num_documents + 2 * num_pairs + 2 <= %zu); use "
+                "maxsim_amd_packed_backward_typed with a workspace",
+                need, kScratchBytes, kScratchBytes / sizeof(int32_t));
+  // The argument checks of the implementation come first, so bad arguments
+  // are rejected without touching the device; the scratch is only needed
+  // when there are pairs to group.
   if (int e = check_dtype(dtype)) return e;
   if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
     return fail(MAXSIM_ERR_INVALID, "grad_dtype must be FLOAT32 or the input dtype");
-  const bool out16 = grad_dtype != MAXSIM_FLOAT32;
-  if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
-      num_documents < 0 || num_pairs < 0)
-    return fail(MAXSIM_ERR_INVALID, "negative size");
+  if (total_q_tokens < 0 || total_d_tokens < 0) return fail(MAXSIM_ERR_INVALID, "negative size");
   if (max_q_len <= 0)
     return fail(MAXSIM_ERR_INVALID, "max_q_len must be > 0; got %lld", (long long)max_q_len);
   if (int e = check_dim(dim)) return e;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if ((total_q_tokens > 0 && !dqueries) || (total_d_tokens > 0 && !ddocuments))
     return fail(MAXSIM_ERR_INVALID, "null gradient pointer");
-  const size_t ws_need =
-      maxsim_amd_packed_backward_workspace_size(num_queries, num_documents, num_pairs);
-  const bool grouped = num_pairs > 0 && workspace && workspace_bytes >= ws_need &&
-                       max_q_len < (1 << 16) && num_pairs < INT32_MAX;
-  // 16-bit gradients are written once per row, which only the grouped
-  // kernels do (the atomic path adds into fp32 rows)
-  if (out16 && num_pairs > 0 && !grouped)
-    return fail(MAXSIM_ERR_UNSUPPORTED,
-                "16-bit gradients need the workspace and max_q_len < 65536; use fp32 gradients");
-  if (!grouped) {
-    if (total_q_tokens > 0) launch_fill_grad(dqueries, total_q_tokens * dim, out16, st);
-    if (total_d_tokens > 0) launch_fill_grad(ddocuments, total_d_tokens * dim, out16, st);
-    if (int e = check_launch("fill_zero_kernel")) return e;
-  }
-  if (num_pairs == 0) return MAXSIM_OK;
-  if (!dscore || !queries || !documents || !query_offsets || !document_offsets ||
-      !pair_query_ids || !pair_document_ids || !argmax)
+  if (num_pairs > 0 && (!dscore || !queries || !documents || !query_offsets ||
+                        !document_offsets || !pair_query_ids || !pair_document_ids || !argmax))
     return fail(MAXSIM_ERR_INVALID, "null pointer argument");
-  const int nslices = (int)((dim + 7) / 8);
-  const int eb = element_bytes(dtype);
-  const bool vec = (dim % 8 == 0) && aligned16b(queries) && aligned16b(documents) &&
-                   ((dim * eb) % 16 == 0);
-  PackedBwdArgs a{};
-  a.dscore = dscore;
-  a.q = queries;
-  a.d = documents;
-  a.qoff = query_offsets;
-  a.doff = document_offsets;
-  a.qids = pair_query_ids;
-  a.dids = pair_document_ids;
-  a.argmax = argmax;
-  a.dq = dqueries;
-  a.dd = ddocuments;
-  a.nq = num_queries;
-  a.nd = num_documents;
-  a.total_q = total_q_tokens;
-  a.total_d = total_d_tokens;
-  a.npairs = num_pairs;
-  a.slots = (int)max_q_len;
-  a.dim = (int)dim;
-  a.nslices = nslices;
-  a.lanes_per_tok = pow2_at_least(nslices < 64 ? nslices : 64);
-  if (!grouped) {
-    MAXSIM_DISPATCH(dtype, launch_packed_bwd, a, vec, st);
-    return check_launch("packed_bwd_kernel");
+  void* ws = nullptr;
+  if (num_pairs > 0) {
+    if (int e = device_scratch(&ws)) return e;
   }
-  // group the pairs by query and by document (counting sort in the workspace)
-  int32_t* w = static_cast<int32_t*>(workspace);
-  PackedGroups g{};
-  g.qstart = w;
-  g.qcur = g.qstart + (num_queries + 1);
-  g.dstart = g.qcur + num_queries;
-  g.dcur = g.dstart + (num_documents + 1);
-  g.qlist = g.dcur + num_documents;
-  g.dlist = g.qlist + num_pairs;
-  // zero qstart..dstart (qcur is written by the scan); fill works on the bits
-  launch_fill(reinterpret_cast<float*>(g.qstart),
-              (num_queries + 1) + num_queries + (num_documents + 1), st);
-  const int64_t pb = std::min<int64_t>((num_pairs + 255) / 256, 2048);
-  hipLaunchKernelGGL(pair_count_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
-  hipLaunchKernelGGL(group_scan_kernel, dim3(2), dim3(kScanThreads), 0, st, g, num_queries,
-                     num_documents);
-  hipLaunchKernelGGL(pair_scatter_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
-  if (int e = check_launch("pair grouping kernels")) return e;
-  if (total_q_tokens > 0)
-    launch_zero_outside(dqueries, out16, query_offsets, num_queries, total_q_tokens, dim, st);
-  if (total_d_tokens > 0)
-    launch_zero_outside(ddocuments, out16, document_offsets, num_documents, total_d_tokens, dim,
-                        st);
-  const int G = pow2_at_least(nslices < 16 ? nslices : 16);  // lanes per dd row
-  const bool vec_g = vec && aligned16b(dqueries) && aligned16b(ddocuments);
-  MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, out16, st);
-  return check_launch("dq_packed_kernel / dd_packed_kernel");
+  return packed_backward_impl(dtype, grad_dtype, dscore, queries, total_q_tokens, query_offsets,
+                              num_queries, documents, total_d_tokens, document_offsets,
+                              num_documents, pair_query_ids, pair_document_ids, num_pairs, argmax,
+                              max_q_len, dim, dqueries, ddocuments, ws, ws ? kScratchBytes : 0,
+                              stream);
 }
 
 int maxsim_amd_packed_backward(
