@@ -57,8 +57,10 @@ enum {
   MAXSIM_ERR_LAUNCH = 3       /* the HIP runtime rejected a launch            */
 };
 
-/* Largest embedding dimension the kernels accept. */
-#define MAXSIM_AMD_MAX_DIM 256
+/* Largest embedding dimension the kernels accept.  Dims up to 256 keep the
+ * query blocks in registers (the fast paths); wider rows are streamed in
+ * K-chunks by the forward and in slice chunks by the backward. */
+#define MAXSIM_AMD_MAX_DIM 16384
 
 int maxsim_amd_abi_version(void);
 const char* maxsim_amd_last_error(void);
@@ -229,7 +231,8 @@ int maxsim_amd_contrastive_forward_with_argmax(
 
 /* Bytes of device workspace that let maxsim_amd_contrastive_backward split
  * the dqueries gather by document range (one range per XCD, partial sums
- * added in a second pass).  0 for invalid sizes.  No counterpart in the
+ * added in a second pass).  0 for invalid sizes and for dim > 2048, where
+ * the backward always takes the single-pass gather.  No counterpart in the
  * reference, whose backward accumulates with global atomics instead. */
 size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
                                                       int64_t dim);

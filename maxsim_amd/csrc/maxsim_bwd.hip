@@ -317,6 +317,7 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 constexpr int kDqBatch = 4;
+constexpr int kDqSplitMaxDim = 2048;  // 8 * 256 slices: one row per workgroup at most
 constexpr int kDqTable = 2048;  // (row, document) pairs staged per chunk
 
 template <typename T, int U>
@@ -617,13 +618,15 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
             if (jj[k] >= 0 && jj[k] < nrows) ids[atomicAdd(&cursor[jj[k]], 1)] = pk[k];
         }
         __syncthreads();
-        // 4. per-row fp32 sums, one group of G lanes per row
-        for (int rr = grp; rr < nrows; rr += ngroups) {
+        // 4. per-row fp32 sums, one group of G lanes per row; a row wider
+        // than NS * G slices (dims above 256 per part) is summed in chunks
+        for (int rr = grp; rr < nrows; rr += ngroups)
+        for (int sc = sl_lo; sc < sl_hi; sc += NS * G) {
           float acc[NS][8];
           void* dst = out_at<O>(a.dd, (d0 + r0 + rr) * (int64_t)a.dim);
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
-            const int sl = sl_lo + gl + u * G;
+            const int sl = sc + gl + u * G;
             if (O::bytes == 4 && sl < sl_hi && !first) {
               load8f<F32>(static_cast<const float*>(dst), sl * 8, a.dim, VEC, acc[u]);
             } else {
@@ -661,7 +664,7 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
               }
 #pragma unroll
               for (int u = 0; u < NS; ++u) {
-                const int sl = sl_lo + gl + u * G;
+                const int sl = sc + gl + u * G;
                 if (sl < sl_hi) {
                   // raw 16-byte fragments, widened to fp32 inside the FMAs
                   Frag<T> v[kDdBatch];
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
           }
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
-            const int sl = sl_lo + gl + u * G;
+            const int sl = sc + gl + u * G;
             if (sl < sl_hi) store8<O>(dst, sl * 8, a.dim, VEC, acc[u]);
           }
         }
@@ -775,10 +778,13 @@ __device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  // a lane covers 4 columns of each 256-column block; wider rows take
+  // several blocks
+  for (int cb = 0; cb < a.dim; cb += 256) {
   int xs[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    xs[i] = a.pair ? 128 * (i >> 1) + 2 * lane + (i & 1) : lane + 64 * i;
+    xs[i] = cb + (a.pair ? 128 * (i >> 1) + 2 * lane + (i & 1) : lane + 64 * i);
   for (int r = r0; r < r1; ++r) {
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (ok && r < ld) {
@@ -837,6 +843,7 @@ __device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t 
       for (int i = 0; i < 4; ++i)
         if (xs[i] < a.dim) row[xs[i]] = to_out16<O>(acc[i]);
     }
+  }
   }
 }
 
@@ -1178,18 +1185,20 @@ __global__ __launch_bounds__(kGroupThreads) void dq_packed_kernel(PackedBwdArgs 
   if (qs < 0 || qe <= qs || qe > a.total_q) return;
   const int lq = (int)(qe - qs);
   const int tid = threadIdx.x;
-  const int rows_per_pass = kGroupThreads / a.nslices;
+  // a row of more than kGroupThreads slices (dims above 2048) is covered in
+  // rounds of kGroupThreads slices, one row per workgroup
+  const int ns = min(a.nslices, kGroupThreads);
+  const int rows_per_pass = kGroupThreads / ns;
   // token block of this workgroup (grid.y covers max_q_len)
   const int i0 = blockIdx.y * rows_per_pass;
   if (i0 >= lq) return;
-  const int local = tid / a.nslices;
-  const int sl = tid - local * a.nslices;
-  const bool active = local < rows_per_pass;
-  const int k0 = sl * 8;
+  const int local = tid / ns;
   const int k_lo = g.qstart[qi], k_hi = g.qstart[qi + 1];
   const bool seg_ok = lq <= a.slots;
   const S* __restrict__ D = static_cast<const S*>(a.d);
-  {
+  for (int sl = tid - local * ns; sl - (tid - local * ns) < a.nslices; sl += ns) {
+    const bool active = local < rows_per_pass && sl < a.nslices;
+    const int k0 = sl * 8;
     const int i = i0 + local;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int c0 = k_lo; seg_ok && c0 < k_hi; c0 += kPairStage) {
@@ -1366,15 +1375,17 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
           }
         }
         __syncthreads();
-        // per-row fp32 sums, one group of G lanes per listed row
+        // per-row fp32 sums, one group of G lanes per listed row; a row wider
+        // than NS * G slices (dims above 256) is summed in chunks
         const int n_rows_full = n_full;
-        for (int i = grp; i < n_rows_full; i += ngroups) {
+        for (int i = grp; i < n_rows_full; i += ngroups)
+        for (int sc = 0; sc < sl_hi; sc += NS * G) {
           const int rr = cursor[i];
           float acc[NS][8];
           void* dst = out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim);
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
-            const int sl = gl + u * G;
+            const int sl = sc + gl + u * G;
             if (O::bytes == 4 && sl < sl_hi && !first) {  // never taken for 16-bit O
               load8f<F32>(static_cast<const float*>(dst), sl * 8, dim, VEC, acc[u]);
             } else {
@@ -1405,7 +1416,7 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
               }
 #pragma unroll
               for (int u = 0; u < NS; ++u) {
-                const int sl = gl + u * G;
+                const int sl = sc + gl + u * G;
                 if (sl < sl_hi) {
                   Frag<T> v[kDdBatch];
 #pragma unroll
@@ -1427,7 +1438,7 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
           }
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
-            const int sl = gl + u * G;
+            const int sl = sc + gl + u * G;
             if (sl < sl_hi) store8<O>(dst, sl * 8, dim, VEC, acc[u]);
           }
         }
@@ -1668,7 +1679,7 @@ template <typename T, typename O>
 static void launch_packed_grouped_o(const PackedBwdArgs& a, const PackedGroups& g, bool vec,
                                     int G, hipStream_t st) {
   if (a.nq > 0) {
-    const int rows_per_pass = kGroupThreads / a.nslices;
+    const int rows_per_pass = kGroupThreads / std::min(a.nslices, kGroupThreads);
     const dim3 grid((unsigned)a.nq, (unsigned)((a.slots + rows_per_pass - 1) / rows_per_pass));
     if (vec)
       hipLaunchKernelGGL((dq_packed_kernel<T, true, O>), grid, dim3(kGroupThreads), 0, st, a, g);
@@ -1893,7 +1904,8 @@ extern "C" {
 
 size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
                                                       int64_t dim) {
-  if (num_queries <= 0 || Lq <= 0 || dim <= 0 || dim > MAXSIM_AMD_MAX_DIM) return 0;
+  // the split pass keeps a workgroup's rows x slices within 256 threads
+  if (num_queries <= 0 || Lq <= 0 || dim <= 0 || dim > kDqSplitMaxDim) return 0;
   return (size_t)kXcds * (size_t)num_queries * (size_t)Lq * (size_t)dim * sizeof(float);
 }
 
@@ -1996,7 +2008,7 @@ int maxsim_amd_contrastive_backward_typed(
   qa.total_d = total_d_tokens;
   qa.padded = 0;
   const size_t ws_need = maxsim_amd_contrastive_backward_workspace_size(num_queries, Lq, dim);
-  if (workspace && workspace_bytes >= ws_need) {
+  if (workspace && ws_need > 0 && workspace_bytes >= ws_need) {
     float* ws = static_cast<float*>(workspace);
     const bool vec_ws = vec && aligned16b(workspace);
     const bool vec_reduce = ((num_queries * Lq * dim) % 4 == 0) && aligned16b(workspace) &&

@@ -255,6 +255,72 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
 }
 
 // ---------------------------------------------------------------------------
+// wide_pair_kernel: embedding dims above kMaxRegDim, where a query block no
+// longer fits in registers.  One wave per pair; each 32x32 tile accumulates
+// over all K-chunks with both operands loaded per chunk (the query block is
+// re-read from L1/L2 for every document tile), kWideBatch chunks in flight.
+// Same tile layout, epilogue and semantics as pair_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kMaxRegDim = 256;  // pair_kernel / tiled kernel: KS <= 16
+constexpr int kWideBatch = 4;
+
+template <typename T, bool ARGMAX, bool VEC>
+__global__ __launch_bounds__(256) void wide_pair_kernel(FwdArgs a) {
+  using S = typename T::storage;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const int64_t p =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (p >= a.npairs) return;
+  const Pair pr = resolve_pair(a, p);
+  if (!pr.ok) {
+    write_invalid_pair(a, p, lane);
+    return;
+  }
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+  const int ks = (dim + kChunk - 1) / kChunk;
+  const int nblk = (pr.lq + kTileCols - 1) / kTileCols;
+  const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
+  float score = 0.0f;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int tok = blk * kTileCols + c;
+    const S* qrow = Q + (pr.q_row0 + min(tok, pr.lq - 1)) * (int64_t)dim;
+    float m = -__builtin_inff();
+    int am = 0;
+    for (int t = 0; t < ntiles; ++t) {
+      // rows past the document end repeat its last row and cannot win
+      const S* drow = D + (pr.d_row0 + min(t * kTileRows + c, pr.ld - 1)) * (int64_t)dim;
+      f32x16 acc = f32x16{};
+      for (int s0 = 0; s0 < ks; s0 += kWideBatch) {
+        Frag<T> fa[kWideBatch], fb[kWideBatch];
+#pragma unroll
+        for (int u = 0; u < kWideBatch; ++u) {
+          const int k0 = kChunk * (s0 + u) + 8 * h;
+          const bool in = s0 + u < ks;
+          fa[u] = in ? load_frag<T>(drow, k0, dim, VEC) : zero_frag<T>();
+          fb[u] = in ? load_frag<T>(qrow, k0, dim, VEC) : zero_frag<T>();
+        }
+#pragma unroll
+        for (int u = 0; u < kWideBatch; ++u)
+          if (s0 + u < ks) mma_chunk(fa[u], fb[u], acc);
+      }
+      tile_update<ARGMAX>(acc, m, am, t * kTileRows + 4 * h);
+    }
+    merge_halves(m, am);
+    const bool valid = tok < pr.lq;
+    score += half_sum(valid ? m : 0.0f);
+    if (ARGMAX && h == 0 && tok < a.slots) a.argmax[p * a.slots + tok] = valid ? am : 0;
+  }
+  if (ARGMAX) {
+    for (int t = nblk * kTileCols + lane; t < a.slots; t += 64) a.argmax[p * a.slots + t] = 0;
+  }
+  if (lane == kHalfSumLane) a.scores[p] = score;
+}
+
+// ---------------------------------------------------------------------------
 // contrastive_tiled_kernel
 // ---------------------------------------------------------------------------
 // Workgroup = 8 waves.  Wave w holds NBW query blocks: queries
@@ -806,8 +872,33 @@ static int pairs_per_wave(int64_t npairs) {
   return (int)ppw;
 }
 
+template <typename T>
+static void launch_wide(const FwdArgs& a, bool vec, hipStream_t st) {
+  const dim3 grid((unsigned)((a.npairs + 3) / 4));
+  if (a.argmax && vec)
+    hipLaunchKernelGGL((wide_pair_kernel<T, true, true>), grid, dim3(256), 0, st, a);
+  else if (a.argmax)
+    hipLaunchKernelGGL((wide_pair_kernel<T, true, false>), grid, dim3(256), 0, st, a);
+  else if (vec)
+    hipLaunchKernelGGL((wide_pair_kernel<T, false, true>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((wide_pair_kernel<T, false, false>), grid, dim3(256), 0, st, a);
+}
+
 static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
                     hipStream_t st) {
+  if (a.dim > kMaxRegDim) {
+    // one wave per pair, four per workgroup
+    if ((a.npairs + 3) / 4 > (int64_t)UINT32_MAX / 256)
+      return fail(MAXSIM_ERR_UNSUPPORTED, "too many pairs for one launch");
+    const bool vec = (a.dim % kChunk == 0) && aligned16(a.q) && aligned16(a.d);
+    switch (dtype) {
+      case MAXSIM_BFLOAT16: launch_wide<BF16>(a, vec, st); break;
+      case MAXSIM_FLOAT16: launch_wide<F16>(a, vec, st); break;
+      default: launch_wide<F32>(a, vec, st); break;
+    }
+    return check_launch("wide_pair_kernel");
+  }
   const int ppw = pairs_per_wave(a.npairs);
   const bool vec = (a.dim == ks_for_dim(a.dim) * kChunk) && aligned16(a.q) &&
                    aligned16(a.d);

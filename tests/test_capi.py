@@ -59,7 +59,9 @@ def test_contrastive_backward_workspace_size(lib):
     # eight fp32 partial copies of dq [Nq, Lq, dim]
     assert fn(512, 32, 128) == 8 * 512 * 32 * 128 * 4
     assert fn(3, 5, 7) == 8 * 3 * 5 * 7 * 4
-    for bad in [(0, 32, 128), (4, 0, 128), (4, 32, 0), (4, 32, 257), (-1, 32, 128)]:
+    assert fn(4, 32, 2048) == 8 * 4 * 32 * 2048 * 4
+    # above 2048 the backward always takes the single-pass gather
+    for bad in [(0, 32, 128), (4, 0, 128), (4, 32, 0), (4, 32, 2049), (-1, 32, 128)]:
         assert fn(*bad) == 0
 
 
@@ -92,8 +94,8 @@ def test_rejects_unknown_dtype(lib):
 def test_rejects_bad_dims(lib):
     assert _contrastive(lib, dim=0) == INVALID
     assert b"dim" in lib.maxsim_amd_last_error()
-    assert _contrastive(lib, dim=4096) == UNSUPPORTED
-    assert b"256" in lib.maxsim_amd_last_error()
+    assert _contrastive(lib, dim=16385) == UNSUPPORTED
+    assert b"16384" in lib.maxsim_amd_last_error()
 
 
 def test_rejects_nonpositive_lq_and_negative_sizes(lib):
