@@ -395,6 +395,287 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, bool vec, float
   if (active) store8f(ws + (int64_t)r * a.rows * a.dim + row * a.dim, k0, a.dim, vec, acc);
 }
 
+// ---------------------------------------------------------------------------
+// dq, contrastive, one pass over the documents in order (document walk).
+//
+// Thread = (query row, 8-element slice); a workgroup holds R rows.  Every
+// workgroup walks all documents in the same order, kWalkTable / R documents
+// per stage: the stage's table of (byte offset of the winning document row,
+// weight) per (row, document) is built in LDS from argmax, offsets and
+// dscore, then each lane gathers its row's winning rows, eight in flight
+// (two 16-byte LDS reads fetch eight offsets, two more eight weights), and
+// adds them in document order in fp32 registers.  A launch's workgroups are
+// resident together and advance at the same rate, so at any moment the
+// workgroups of one XCD gather from the same few documents, which its L2
+// holds; D is streamed through each L2 once.  dq is written once in the
+// output type O: no partial sums, no workspace, no second pass, and the
+// order of the additions (documents ascending, one fmaf each) is the one
+// dq_gather_kernel uses, so the two agree bit for bit.
+//
+// OFF32: D is smaller than 2 GiB, so the table holds 32-bit byte offsets
+// (invalid entries -1) and a gather address is one add.  Otherwise the table
+// holds row indices and the address is computed in 64 bits.
+// ---------------------------------------------------------------------------
+constexpr int kWalkTable = 2048;   // (row, document) entries per stage
+constexpr int kWalkMaxRows = 32;   // rows per workgroup at most
+constexpr int kWalkPad = 4;        // table row stride = docs per stage + 4 (ints)
+constexpr int kWalkTableInts = kWalkTable + kWalkPad * kWalkMaxRows;
+
+template <typename T, bool VEC, bool OFF32, typename O>
+__global__ __launch_bounds__(256) void dq_walk_kernel(DqArgs a, int rows_per_group) {
+  using S = typename T::storage;
+  __shared__ __align__(16) int32_t t_src[kWalkTableInts];
+  __shared__ __align__(16) float t_w[kWalkTableInts];
+  const int R = rows_per_group;
+  const int dps = kWalkTable / R;  // documents per stage, a multiple of 8
+  const int stride = dps + kWalkPad;
+  const int tid = threadIdx.x;
+  const int64_t row0 = (int64_t)blockIdx.x * R;
+  const int lr = tid / a.nslices;
+  const int sl = tid - lr * a.nslices;
+  const int64_t row = row0 + lr;
+  const bool active = lr < R && row < a.rows;
+  const int k0 = sl * 8;
+  const uint32_t row_bytes = (uint32_t)a.dim * (uint32_t)sizeof(S);
+  const char* __restrict__ Db = static_cast<const char*>(a.d);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int tab = lr * stride;  // this lane's table row
+
+  const uint32_t k0b = (uint32_t)k0 * (uint32_t)sizeof(S);
+  auto gather = [&](int32_t src) -> Frag<T> {
+    if constexpr (OFF32 && VEC) {
+      // uniform base + one 32-bit offset per lane (the saddr form)
+      const uint4* p = reinterpret_cast<const uint4*>(Db + ((uint32_t)src + k0b));
+      Frag<T> f;
+      if constexpr (T::bytes == 2) {
+        f.v = p[0];
+      } else {
+        f.lo = p[0];
+        f.hi = p[1];
+      }
+      return f;
+    } else if constexpr (OFF32) {
+      return load_frag<T>(reinterpret_cast<const S*>(Db + (uint32_t)src), k0, a.dim, VEC);
+    } else {
+      return load_frag<T>(D + (int64_t)src * a.dim, k0, a.dim, VEC);
+    }
+  };
+  auto add = [&](const Frag<T>& v, float w) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, frag_elem(v, e), acc[e]);
+  };
+
+  for (int64_t b0 = 0; b0 < a.nb; b0 += dps) {
+    const int nd = (int)min((int64_t)dps, a.nb - b0);
+    __syncthreads();  // the previous stage's table is consumed
+    // consecutive threads take consecutive rows of one document: the argmax
+    // reads of a query's tokens are contiguous
+    for (int e = tid; e < R * dps; e += 256) {
+      const int d = e / R;
+      const int r = e - d * R;
+      const int64_t rw = row0 + r;
+      int32_t src = -1;
+      float w = 0.0f;
+      if (d < nd && rw < a.rows) {
+        const int64_t qidx = rw / a.lq;
+        const int i = (int)(rw - qidx * a.lq);
+        const int64_t b = b0 + d;
+        const int64_t s0 = a.doff[b], s1 = a.doff[b + 1];
+        const int j = a.argmax[(qidx * a.nb + b) * a.lq + i];
+        if (s0 >= 0 && s1 > s0 && s1 <= a.total_d && j >= 0 && j < s1 - s0) {
+          src = OFF32 ? (int32_t)((uint32_t)(s0 + j) * row_bytes) : (int32_t)(s0 + j);
+          w = a.dscore[qidx * a.nb + b];
+        }
+      }
+      t_src[r * stride + d] = src;
+      t_w[r * stride + d] = w;
+    }
+    __syncthreads();
+    if (!active) continue;
+    int d = 0;
+    // eight documents per step; a step holding an invalid entry (or past
+    // the stage's end) takes the masked form, which skips such entries
+    for (; d < nd; d += 8) {
+      // tab and d are multiples of 4: 16-byte LDS reads
+      const int4* sp = static_cast<const int4*>(__builtin_assume_aligned(&t_src[tab + d], 16));
+      const float4* wp = static_cast<const float4*>(__builtin_assume_aligned(&t_w[tab + d], 16));
+      const int4 s_lo = sp[0], s_hi = sp[1];
+      const float4 w_lo = wp[0], w_hi = wp[1];
+      const int32_t s[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+      const float w[8] = {w_lo.x, w_lo.y, w_lo.z, w_lo.w, w_hi.x, w_hi.y, w_hi.z, w_hi.w};
+      int32_t smin = s[0];
+#pragma unroll
+      for (int u = 1; u < 8; ++u) smin = min(smin, s[u]);
+      if (__all(smin >= 0) && d + 8 <= nd) {
+        Frag<T> v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = gather(s[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) add(v[u], w[u]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (d + u < nd && s[u] >= 0) add(gather(s[u]), w[u]);
+        }
+      }
+    }
+  }
+  if (active) store8<O>(out_at<O>(a.dq, row * a.dim), k0, a.dim, VEC, acc);
+}
+
+// ---------------------------------------------------------------------------
+// dq, contrastive, one document range per XCD, all of an XCD's workgroups
+// resident at once (dq_range_kernel).
+//
+// Random 16-byte gathers run at about 30 TB/s from L2 but 7-8 TB/s once
+// they miss it (the MALL helps little for them), so the gather's working
+// set must fit an XCD's 4 MB L2.  Documents are split into kXcds ranges,
+// range r gathered only by the workgroups of XCD r (workgroup w runs on XCD
+// w % 8), and the launch is one round (1024 workgroups of 128 rows at C5,
+// four per CU), every workgroup walking its range's documents in order: the
+// workgroups of an XCD then gather from the same few documents at any
+// moment, and D is fetched from HBM about once.
+//
+// A wave holds 8 * 64 / NSL rows (NSL lanes per row, one 8-element slice
+// each); a lane owns kRangeItems consecutive rows of one query (Lq % 8 ==
+// 0).  Each stage of a workgroup first copies its rows' argmax for a chunk
+// of documents into LDS with direct global->LDS loads (document-major, 32
+// KB), and the chunk's weights and offsets with ordinary loads, so the walk
+// waits on no HBM latency: per document a lane reads its rows' winners with
+// two 16-byte LDS reads and issues eight gathers whose addresses are one
+// multiply-add each.  The partial sums of range r go to ws[r];
+// dq_reduce_kernel adds the kXcds parts in range order.
+// ---------------------------------------------------------------------------
+constexpr int kRangeItems = 8;
+constexpr int kRangeTableInts = 8192;              // argmax entries staged per stage (32 KB)
+constexpr int kRangeMaxQueries = 2048 / 8 + 1;     // queries one workgroup's rows can touch
+
+// Four waves per SIMD (<= 128 VGPRs) keep the launch one round at C5.
+template <typename T, int NSL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void dq_range_kernel(DqArgs a, float* __restrict__ ws) {
+  using S = typename T::storage;
+  constexpr int RPW = (64 / NSL) * kRangeItems;    // rows per wave
+  constexpr int RW = 4 * RPW;                      // rows per workgroup
+  constexpr int DC = kRangeTableInts / RW;         // documents per stage
+  constexpr int QW = RW / 8 + 1;                   // queries per workgroup, at most
+  __shared__ __align__(16) int32_t t_j[kRangeTableInts];  // [document][row]
+  __shared__ float t_g[DC * QW];                          // [document][query]
+  __shared__ int32_t t_off[DC + 1];
+  const int r = blockIdx.x % kXcds;
+  const int64_t row0 = (int64_t)(blockIdx.x / kXcds) * RW;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int sub = lane / NSL;
+  const int sl = lane - sub * NSL;
+  const int lr0 = wave * RPW + sub * kRangeItems;  // this lane's first row in the workgroup
+  const int64_t row_base = row0 + lr0;
+  const bool rows_ok = row_base < a.rows;          // all 8 rows valid: rows % 8 == 0
+  const int64_t q_first = row0 / a.lq;
+  const int q_lane = rows_ok ? (int)(row_base / a.lq - q_first) : 0;
+  const int64_t b_lo = a.nb * r / kXcds;
+  const int64_t b_hi = a.nb * (r + 1) / kXcds;
+  const uint32_t row_bytes = (uint32_t)a.dim * (uint32_t)sizeof(S);
+  const uint32_t k0b = (uint32_t)sl * 8u * (uint32_t)sizeof(S);
+  const char* __restrict__ Db = static_cast<const char*>(a.d);
+  const uint32_t lds_j = __builtin_amdgcn_readfirstlane(lds_addr(t_j));
+  float acc[kRangeItems][8];
+#pragma unroll
+  for (int u = 0; u < kRangeItems; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[u][e] = 0.0f;
+
+  for (int64_t c0 = b_lo; c0 < b_hi; c0 += DC) {
+    const int nd = (int)min((int64_t)DC, b_hi - c0);
+    __syncthreads();  // the previous stage's tables are consumed
+    // argmax of the stage: LDS byte o holds document o / (4 RW), row
+    // (o % (4 RW)) / 4 of the workgroup; a lane's 16 bytes are 4 consecutive
+    // rows of one (query, document).  Entries past the stage's documents or
+    // the last row are read from the start of argmax and never used.
+    constexpr int kInstrs = kRangeTableInts * 4 / 1024;  // 1 KB per wave instruction
+    for (int k = wave; k < kInstrs; k += 4) {
+      const int o = k * 1024 + lane * 16;
+      const int d = o / (RW * 4);
+      const int64_t rw = row0 + (o - d * RW * 4) / 4;
+      uint32_t src = 0;
+      if (d < nd && rw < a.rows) {
+        const int64_t q = rw / a.lq;
+        src = (uint32_t)(((q * a.nb + c0 + d) * a.lq + (rw - q * a.lq)) * 4);
+      }
+      lds_dma16(a.argmax, src, lds_j + (uint32_t)k * 1024u);
+    }
+    for (int x = tid; x < nd * QW; x += 256) {
+      const int d = x / QW;
+      const int64_t q = q_first + (x - d * QW);
+      t_g[x] = q < a.rows / a.lq ? a.dscore[q * a.nb + c0 + d] : 0.0f;
+    }
+    for (int x = tid; x <= nd; x += 256) t_off[x] = a.doff[c0 + x];
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies landed
+    __syncthreads();
+    if (!rows_ok) continue;
+    for (int d = 0; d < nd; ++d) {
+      const int4* jp = static_cast<const int4*>(__builtin_assume_aligned(&t_j[d * RW + lr0], 16));
+      const int4 jlo = jp[0], jhi = jp[1];
+      const int j[kRangeItems] = {jlo.x, jlo.y, jlo.z, jlo.w, jhi.x, jhi.y, jhi.z, jhi.w};
+      const float g = t_g[d * QW + q_lane];
+      const int s0 = __builtin_amdgcn_readfirstlane(t_off[d]);
+      const int s1 = __builtin_amdgcn_readfirstlane(t_off[d + 1]);
+      const bool doc_ok = s0 >= 0 && s1 > s0 && (int64_t)s1 <= a.total_d;
+      const uint32_t len = doc_ok ? (uint32_t)(s1 - s0) : 0u;
+      // every index is clamped into the document (an invalid document reads
+      // row 0 of D), so each address is one min and one 24-bit multiply-add
+      // (document lengths and row sizes are below 2^24)
+      // (readfirstlane keeps the bound a scalar, so the clamp is one v_min)
+      const uint32_t last = __builtin_amdgcn_readfirstlane(doc_ok ? len - 1u : 0u);
+      const uint32_t base =
+          __builtin_amdgcn_readfirstlane(doc_ok ? (uint32_t)s0 * row_bytes : 0u) + k0b;
+      uint32_t jmax = (uint32_t)j[0];
+#pragma unroll
+      for (int u = 1; u < kRangeItems; ++u) jmax = max(jmax, (uint32_t)j[u]);
+      // An out-of-range argmax (every entry of an invalid document) is
+      // skipped, as the reference's guard does: the rare step that holds one
+      // zeroes that fragment and its weight, so the additions below are the
+      // same instructions either way.
+      const bool all_ok = __all(jmax < len);
+      Frag<T> v[kRangeItems];
+      float w[kRangeItems];
+#pragma unroll
+      for (int u = 0; u < kRangeItems; ++u) {
+        const uint32_t ju = min((uint32_t)j[u], last);
+        const uint4* p = reinterpret_cast<const uint4*>(Db + (__umul24(ju, row_bytes) + base));
+        if constexpr (T::bytes == 2) {
+          v[u].v = p[0];
+        } else {
+          v[u].lo = p[0];
+          v[u].hi = p[1];
+        }
+        w[u] = g;
+      }
+      if (!all_ok) {
+#pragma unroll
+        for (int u = 0; u < kRangeItems; ++u) {
+          if ((uint32_t)j[u] >= len) {
+            v[u] = zero_frag<T>();
+            w[u] = 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRangeItems; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[u][e] = fmaf(w[u], frag_elem(v[u], e), acc[u][e]);
+    }
+  }
+  if (rows_ok) {
+#pragma unroll
+    for (int u = 0; u < kRangeItems; ++u)
+      store8f(ws + (int64_t)r * a.rows * a.dim + (row_base + u) * a.dim, sl * 8, a.dim, true,
+              acc[u]);
+  }
+}
+
 // dq[x] = sum over the kXcds partial buffers, in range order, written in
 // the output type O.
 template <typename O>
@@ -699,6 +980,212 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
         __syncthreads();
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dd, contrastive, the common case (dd_bucket_kernel): rows of 16-byte
+// fragments, dim <= 256 per part with an even number of 8-element slices,
+// every (query, token) entry of a document in one LDS pass, Q below 2 GiB.
+// Same counting sort and blocked row sums as dd_contrastive_kernel, with
+// less work per entry:
+//   * the document's argmax entries stay in registers between the
+//     histogram and the scatter (one read of argmax instead of two), and
+//     the (query, token) of an entry needs no division: a thread's entries
+//     are x = tid + 512 k, so when Lq divides 512 the token is fixed and the
+//     query advances by 512 / Lq;
+//   * a lane owns two slices (16 elements) of its group's row, so an
+//     entry's decode (row offset, weight) is shared by 16 elements;
+//   * Q rows are addressed as one 32-bit offset from a uniform base (one
+//     24-bit multiply-add per entry), and four entries (eight 16-byte
+//     loads) are in flight per lane.
+// ---------------------------------------------------------------------------
+constexpr int kBkBatch = 8;            // bucket entries gathered per step
+constexpr int kBkMaxEntriesPerThread = 32;
+
+template <typename T, int NS, typename O>
+__global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
+  using S = typename T::storage;
+  extern __shared__ int lds_i[];
+  const int R = a.rows_per_pass;
+  const int E = a.entries_per_pass;
+  int* start = lds_i;                 // [R + 1]
+  int* cursor = start + (R + 1);      // [R + 1]
+  int* ids = cursor + (R + 1);        // [E]
+  float* gst = reinterpret_cast<float*>(ids + E);  // [Nq]
+
+  const int xcd = blockIdx.x % kXcds;
+  const int per_part = kXcds / a.parts;
+  const int part = xcd / per_part;
+  const int64_t b = (int64_t)(blockIdx.x / kXcds) * per_part + xcd % per_part;
+  if (b >= a.nb) return;
+  if (part == 0 && (b == 0 || b == a.nb - 1)) {
+    const int64_t head = min(max((int64_t)a.doff[0], (int64_t)0), a.total_d);
+    const int64_t tail = min(max((int64_t)a.doff[a.nb], head), a.total_d);
+    auto zero_rows = [&](int64_t lo, int64_t hi) {
+      for (int64_t x = lo * a.dim + threadIdx.x; x < hi * a.dim; x += kDdThreads) {
+        if constexpr (O::bytes == 4)
+          static_cast<float*>(a.dd)[x] = 0.0f;
+        else
+          static_cast<uint16_t*>(a.dd)[x] = 0;
+      }
+    };
+    if (b == 0) zero_rows(0, head);
+    if (b == a.nb - 1) zero_rows(tail, a.total_d);
+  }
+  const int64_t d0 = a.doff[b], d1 = a.doff[b + 1];
+  if (d0 < 0 || d1 <= d0 || d1 > a.total_d) return;
+  const int ld = (int)(d1 - d0);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int G = a.group;               // lanes per row; each lane owns NS slices
+  const int ngroups = kDdThreads / G;
+  const int grp = tid / G;
+  const int gl = tid - grp * G;
+  const int sl_lo = part * a.part_slices;
+  const int sl_hi = min(sl_lo + a.part_slices, a.nslices);
+  const int ne = (int)(a.nq * a.lq);   // every entry in one pass (host checks)
+  const int32_t* am_b = a.argmax + b * a.lq;
+  const int am_qstride = (int)(a.nb * a.lq);  // argmax below 2^31 entries (host checks)
+  const MAXSIM_GLOBAL char* Qb = uniform_gptr(static_cast<const char*>(a.q));
+  const uint32_t row_bytes = (uint32_t)a.dim * (uint32_t)sizeof(S);
+  // this lane's NS consecutive slices of a row, from sc (the host makes a
+  // part exactly NS * G slices)
+  const int sc = sl_lo + NS * gl;
+  const uint32_t k0b = (uint32_t)sc * 8u * (uint32_t)sizeof(S);
+  (void)sl_hi;
+  // A thread's entries are x = tid + 512 k.  Lq divides 512 (host checks),
+  // so every one of them has token tid % Lq and the query advances by
+  // 512 / Lq: the argmax of entry k is one uniform base plus a 32-bit offset
+  // that grows by a fixed step.
+  const int q_t = tid / a.lq;
+  const int i_t = tid - q_t * a.lq;
+  const int q_step = kDdThreads / a.lq;
+  const MAXSIM_GLOBAL char* amB = uniform_gptr(reinterpret_cast<const char*>(am_b));
+  const uint32_t off_t = (uint32_t)(q_t * am_qstride + i_t) * 4u;
+  const uint32_t off_step = (uint32_t)(q_step * am_qstride) * 4u;
+  const uint32_t off_last = (uint32_t)((a.nq - 1) * am_qstride + (a.lq - 1)) * 4u;
+  for (int x = tid; x < a.nq; x += kDdThreads) gst[x] = a.dscore[x * a.nb + b];
+
+  // entries of this thread with a valid query: k < nk
+  const int nk_t = min((int)((a.nq - q_t + q_step - 1) / q_step), kBkMaxEntriesPerThread);
+  for (int r0 = 0; r0 < ld; r0 += R) {
+    const int nrows = min(R, ld - r0);
+    // Opaque per pass: otherwise the compiler hoists every entry's validity
+    // mask and packed id out of the pass loop (64 SGPRs, 32 VGPRs, spills).
+    int nk = nk_t, qt = q_t, xt = tid;
+    uint32_t offt = off_t;
+    __asm__ __volatile__("" : "+v"(nk), "+v"(qt), "+v"(xt), "+v"(offt));
+    for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
+    __syncthreads();
+    // 1. read this thread's entries (all issued before the first atomic;
+    // entries past the last query re-read the last entry and are dropped)
+    // and histogram their target rows
+    int jj[kBkMaxEntriesPerThread];
+#pragma unroll
+    for (int k = 0; k < kBkMaxEntriesPerThread; ++k) {
+      const uint32_t off = min(offt + (uint32_t)k * off_step, off_last);
+      const int v = *reinterpret_cast<const MAXSIM_GLOBAL int*>(amB + off);
+      jj[k] = k < nk ? v - r0 : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kBkMaxEntriesPerThread; ++k)
+      if (jj[k] >= 0 && jj[k] < nrows) atomicAdd(&start[jj[k] + 1], 1);
+    __syncthreads();
+    // 2. inclusive scan of start[1..nrows] by wave 0 (a lane owns a run)
+    if (tid < 64) {
+      const int per = (nrows + 63) / 64;
+      const int lo = 1 + lane * per;
+      const int hi = min(lo + per, nrows + 1);
+      int run = 0;
+      for (int x = lo; x < hi; ++x) run += start[x];
+      int incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
+      }
+      int acc = incl - run;
+      for (int x = lo; x < hi; ++x) {
+        acc += start[x];
+        start[x] = acc;
+      }
+    }
+    __syncthreads();
+    for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
+    __syncthreads();
+    // 3. scatter packed entry ids (x | query << 16) from the registers
+#pragma unroll
+    for (int k = 0; k < kBkMaxEntriesPerThread; ++k) {
+      if (jj[k] >= 0 && jj[k] < nrows) {
+        const int x = xt + k * kDdThreads;
+        ids[atomicAdd(&cursor[jj[k]], 1)] = x | ((qt + k * q_step) << 16);
+      }
+    }
+    __syncthreads();
+    // 4. per-row fp32 sums: a group of G lanes per row, two slices per lane
+    for (int rr = grp; rr < nrows; rr += ngroups) {
+      float acc[NS][8];
+#pragma unroll
+      for (int u = 0; u < NS; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[u][e] = 0.0f;
+      void* dst = out_at<O>(a.dd, (d0 + r0 + rr) * (int64_t)a.dim);
+      const int s_end = start[rr + 1];
+      for (int s0 = start[rr]; s0 < s_end; s0 += kDdBlock) {
+        const int s1 = min(s0 + kDdBlock, s_end);
+        float blk[NS][8];
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) blk[u][e] = 0.0f;
+        auto batch = [&](int s, auto masked) {
+          constexpr bool MASKED = decltype(masked)::value;
+          uint32_t off[kBkBatch];
+          float gx[kBkBatch];
+          bool ok[kBkBatch];
+#pragma unroll
+          for (int k = 0; k < kBkBatch; ++k) {
+            ok[k] = !MASKED || s + k < s1;
+            const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
+            off[k] = __umul24(v & 0xffffu, row_bytes) + k0b;
+            gx[k] = gst[v >> 16];
+          }
+          Frag<T> f[kBkBatch][NS];
+#pragma unroll
+          for (int k = 0; k < kBkBatch; ++k)
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+              const uint32_t o = off[k] + (uint32_t)u * 8u * (uint32_t)sizeof(S);
+              if constexpr (T::bytes == 2) {
+                f[k][u].v = load16(Qb, o);
+              } else {
+                f[k][u].lo = load16(Qb, o);
+                f[k][u].hi = load16(Qb, o + 16u);
+              }
+            }
+#pragma unroll
+          for (int k = 0; k < kBkBatch; ++k)
+#pragma unroll
+            for (int u = 0; u < NS; ++u)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float t = fmaf(gx[k], frag_elem(f[k][u], e), blk[u][e]);
+                blk[u][e] = (!MASKED || ok[k]) ? t : blk[u][e];
+              }
+        };
+        int s = s0;
+        for (; s + kBkBatch <= s1; s += kBkBatch) batch(s, std::false_type{});
+        if (s < s1) batch(s, std::true_type{});
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[u][e] += blk[u][e];
+      }
+#pragma unroll
+      for (int u = 0; u < NS; ++u) store8<O>(dst, (sc + u) * 8, a.dim, true, acc[u]);
+    }
+    __syncthreads();
   }
 }
 
@@ -1588,6 +2075,69 @@ static void launch_dq(const DqArgs& a, bool vec, bool out16, hipStream_t st) {
     hipLaunchKernelGGL((dq_gather_kernel<T, F32>), grid, dim3(256), 0, st, a, vec);
 }
 
+// Rows per workgroup of dq_walk_kernel: a power of two, at most
+// kWalkMaxRows, with rows x slices <= 256 threads.
+static int walk_rows(int nslices) {
+  int r = kWalkMaxRows;
+  while (r > 1 && r * nslices > 256) r >>= 1;
+  return r;
+}
+
+template <typename T>
+static void launch_dq_walk(const DqArgs& a, bool vec, bool off32, bool out16, hipStream_t st) {
+  const int R = walk_rows(a.nslices);
+  const dim3 grid((unsigned)((a.rows + R - 1) / R));
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a, R); };
+  if (out16) {
+    if (vec && off32) go(dq_walk_kernel<T, true, true, T>);
+    else if (vec) go(dq_walk_kernel<T, true, false, T>);
+    else if (off32) go(dq_walk_kernel<T, false, true, T>);
+    else go(dq_walk_kernel<T, false, false, T>);
+  } else {
+    if (vec && off32) go(dq_walk_kernel<T, true, true, F32>);
+    else if (vec) go(dq_walk_kernel<T, true, false, F32>);
+    else if (off32) go(dq_walk_kernel<T, false, true, F32>);
+    else go(dq_walk_kernel<T, false, false, F32>);
+  }
+}
+
+// dq_range_kernel covers vec rows of 2^k slices (dims 8..256), Lq % 8 == 0
+// and D below 2 GiB (32-bit byte offsets); returns false otherwise.
+template <typename T>
+static bool launch_dq_range(const DqArgs& a, float* ws, bool vec, bool off32, bool vec_reduce,
+                            bool out16, hipStream_t st) {
+  // fp32 fragments do not fit four waves per SIMD: dq_split_kernel takes fp32
+  if constexpr (T::bytes == 4) {
+    return false;
+  } else {
+  // 32-bit byte offsets for D (off32) and for argmax (the staging copies)
+  const int ns = a.nslices;
+  if (!vec || !off32 || a.lq % kRangeItems != 0 || ns > 32 || (ns & (ns - 1)) != 0 ||
+      a.rows * a.nb * (int64_t)sizeof(int32_t) >= ((int64_t)1 << 31))
+    return false;
+  const int rpw = (64 / a.nslices) * kRangeItems;
+  const int64_t wgs = (a.rows + 4 * rpw - 1) / (4 * rpw);
+  const dim3 grid((unsigned)(wgs * kXcds));
+  switch (a.nslices) {
+    case 1: hipLaunchKernelGGL((dq_range_kernel<T, 1>), grid, dim3(256), 0, st, a, ws); break;
+    case 2: hipLaunchKernelGGL((dq_range_kernel<T, 2>), grid, dim3(256), 0, st, a, ws); break;
+    case 4: hipLaunchKernelGGL((dq_range_kernel<T, 4>), grid, dim3(256), 0, st, a, ws); break;
+    case 8: hipLaunchKernelGGL((dq_range_kernel<T, 8>), grid, dim3(256), 0, st, a, ws); break;
+    case 16: hipLaunchKernelGGL((dq_range_kernel<T, 16>), grid, dim3(256), 0, st, a, ws); break;
+    case 32: hipLaunchKernelGGL((dq_range_kernel<T, 32>), grid, dim3(256), 0, st, a, ws); break;
+    default: return false;
+  }
+  const int64_t n = a.rows * a.dim;
+  const int64_t work = vec_reduce ? n / 4 : n;
+  const dim3 rgrid((unsigned)std::max<int64_t>(std::min<int64_t>((work + 255) / 256, 4096), 1));
+  if (out16)
+    hipLaunchKernelGGL(dq_reduce_kernel<T>, rgrid, dim3(256), 0, st, ws, a.dq, n, vec_reduce);
+  else
+    hipLaunchKernelGGL(dq_reduce_kernel<F32>, rgrid, dim3(256), 0, st, ws, a.dq, n, vec_reduce);
+  return true;
+  }
+}
+
 template <typename T>
 static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduce, bool out16,
                             hipStream_t st) {
@@ -1637,6 +2187,32 @@ static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st)
   const int64_t per_part = kXcds / a.parts;
   const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
+}
+
+template <typename T, typename O>
+static void launch_dd_bucket_o(const DdArgs& a, size_t lds, hipStream_t st) {
+  const auto kern = dd_bucket_kernel<T, 1, O>;
+  if (lds > 64 * 1024) {
+    static bool raised[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !raised[dev]) {
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)max_lds_per_block());
+      (void)hipGetLastError();
+      if (dev >= 0 && dev < 64) raised[dev] = true;
+    }
+  }
+  const int64_t per_part = kXcds / a.parts;
+  const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
+}
+
+template <typename T>
+static void launch_dd_bucket(const DdArgs& a, size_t lds, bool out16, hipStream_t st) {
+  if (out16)
+    launch_dd_bucket_o<T, T>(a, lds, st);
+  else
+    launch_dd_bucket_o<T, F32>(a, lds, st);
 }
 
 template <typename T, typename O>
@@ -2008,18 +2584,53 @@ int maxsim_amd_contrastive_backward_typed(
   qa.total_d = total_d_tokens;
   qa.padded = 0;
   const size_t ws_need = maxsim_amd_contrastive_backward_workspace_size(num_queries, Lq, dim);
+  // 32-bit byte offsets of D rows when D is below 2 GiB
+  const bool off32 = total_d_tokens * dim * eb < ((int64_t)1 << 31);
   if (workspace && ws_need > 0 && workspace_bytes >= ws_need) {
     float* ws = static_cast<float*>(workspace);
     const bool vec_ws = vec && aligned16b(workspace);
     const bool vec_reduce = ((num_queries * Lq * dim) % 4 == 0) && aligned16b(workspace) &&
                             aligned16b(dqueries);
-    MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, out16, st);
-    if (int e = check_launch("dq_split_kernel")) return e;
+    bool done = false;
+    switch (dtype) {
+      case MAXSIM_BFLOAT16: done = launch_dq_range<BF16>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
+      case MAXSIM_FLOAT16: done = launch_dq_range<F16>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
+      default: done = launch_dq_range<F32>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
+    }
+    if (!done) MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, out16, st);
+    if (int e = check_launch("dq_range_kernel / dq_split_kernel")) return e;
+  } else if (nslices <= 256) {
+    MAXSIM_DISPATCH(dtype, launch_dq_walk, qa, vec, off32, out16, st);
+    if (int e = check_launch("dq_walk_kernel")) return e;
   } else {
     MAXSIM_DISPATCH(dtype, launch_dq, qa, vec, out16, st);
     if (int e = check_launch("dq_gather_kernel")) return e;
   }
 
+  // dd_bucket_kernel: every entry of a document in one pass, held 32 per
+  // thread, and parts of exactly 2 * G slices with G a power of two <= 16
+  {
+    const int64_t ne_all = num_queries * Lq;
+    const int g2 = da.part_slices;  // one slice per lane
+    const bool bucket = vec && kDdThreads % Lq == 0 && g2 >= 1 &&
+                        g2 <= kDdMaxGroup &&
+                        (g2 & (g2 - 1)) == 0 && da.part_slices * da.parts == nslices &&
+                        ne_all <= (int64_t)kDdThreads * kBkMaxEntriesPerThread &&
+                        q_bytes < ((int64_t)1 << 31) &&
+                        num_queries * num_documents * Lq < ((int64_t)1 << 31);
+    if (bucket) {
+      DdArgs ba = da;
+      ba.group = g2;
+      ba.rows_per_pass = 1024;
+      ba.entries_per_pass = (int)ne_all;
+      const size_t blds = 2 * (size_t)(ba.rows_per_pass + 1) * sizeof(int) +
+                          ((size_t)ne_all + (size_t)num_queries) * sizeof(int);
+      if (blds <= max_lds_per_block()) {
+        MAXSIM_DISPATCH(dtype, launch_dd_bucket, ba, blds, out16, st);
+        return check_launch("dd_bucket_kernel");
+      }
+    }
+  }
   MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, out16, st);
   return check_launch("dd_contrastive_kernel");
 }

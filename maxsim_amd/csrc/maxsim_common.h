@@ -237,4 +237,52 @@ __device__ __forceinline__ float half_sum(float v) {
   return dpp_add<0x142, 0xA>(v);
 }
 
+// A global-memory pointer the caller knows to be the same in every lane,
+// read back as a scalar and typed in the global address space: loads
+// through it with a 32-bit per-lane offset then take the saddr form
+// (uniform base in SGPRs + one VGPR offset) instead of a 64-bit address per
+// lane.
+#define MAXSIM_GLOBAL __attribute__((address_space(1)))
+template <typename P>
+__device__ __forceinline__ const MAXSIM_GLOBAL P* uniform_gptr(const P* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const MAXSIM_GLOBAL P*)(((uint64_t)hi << 32) | lo);
+}
+
+// 16 bytes at base + off (off a multiple of 16) through a global pointer.
+__device__ __forceinline__ uint4 load16(const MAXSIM_GLOBAL char* base, uint32_t off) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = *reinterpret_cast<const MAXSIM_GLOBAL u32x4*>(base + off);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// 32-bit LDS byte address of an LDS pointer (generic -> LDS address space).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+
+// One wave instruction moving 16 bytes per lane from global memory
+// (uniform base + per-lane 32-bit byte offset) straight into LDS at
+// m0 + 16 * lane.  m0 is an input operand of the asm ("{m0}"), so the
+// compiler itself writes it just before the instruction and knows it is
+// read; nothing reserved is clobbered behind its back.  The compiler's
+// hazard recognizer does not look inside inline asm, so the asm opens with
+// s_nop 4: five wait states cover both a VALU write (readfirstlane) of the
+// base SGPRs, which a VMEM read needs five states after, and the compiler's
+// SALU write of m0, which an LDS DMA needs one state after.
+// (__builtin_amdgcn_global_load_lds would need no asm, but then the
+// compiler puts an s_waitcnt vmcnt(0) before every LDS read that follows a
+// DMA, since it cannot tell the ring buffers apart, which serialises the
+// ring.)
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
+  __asm__ __volatile__(
+      "s_nop 4\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(m0))
+      : "memory");
+}
+
 }  // namespace maxsim

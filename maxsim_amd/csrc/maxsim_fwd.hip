@@ -371,32 +371,6 @@ __device__ __forceinline__ int opaque(int v) {
   return v;
 }
 
-// 32-bit LDS byte address of an LDS pointer (generic -> LDS address space).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
-}
-
-// One wave instruction moving 16 bytes per lane from global memory
-// (uniform base + per-lane 32-bit byte offset) straight into LDS at
-// m0 + 16 * lane.  m0 is an input operand of the asm ("{m0}"), so the
-// compiler itself writes it just before the instruction and knows it is
-// read; nothing reserved is clobbered behind its back.  The compiler's
-// hazard recognizer does not look inside inline asm, so the asm opens with
-// s_nop 4: five wait states cover both a VALU write (readfirstlane) of the
-// base SGPRs, which a VMEM read needs five states after, and the compiler's
-// SALU write of m0, which an LDS DMA needs one state after.
-// (__builtin_amdgcn_global_load_lds would need no asm, but then the
-// compiler puts an s_waitcnt vmcnt(0) before every LDS read that follows a
-// DMA, since it cannot tell the ring buffers apart, which serialises the
-// ring.)
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t m0) {
-  __asm__ __volatile__(
-      "s_nop 4\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(m0))
-      : "memory");
-}
 
 template <typename T, int KS>
 struct TileGeom {
