@@ -9,8 +9,10 @@ diagonal, backward to dQ and dD.  Inputs are resident in HBM before timing.
 Printed as ONE JSON line.  ``value`` is the step throughput in TFLOP/s
 (F = 2*D*Nq*Lq*T_d forward flops per step / step time); ``ms_per_step`` is the
 user-level step time (including the API's offset validation).
-Kernel-level timings, the other configurations (C2 contrastive 64x64, C3
-padded rerank docs/s, C4 packed pairs) and the CPU baseline are extra fields.
+``extra.c5.fused_ce_step_ms`` is the same step through the fused loss
+(score_contrastive_cross_entropy).  Kernel-level timings, the other
+configurations (C2 contrastive 64x64, C3 padded rerank docs/s, C4 packed
+pairs) and the CPU baseline are extra fields.
 
     python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -464,6 +466,24 @@ def main():
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / K
 
+    # the same step through the fused loss (softmax gradient recomputed inside
+    # the backward kernels, no dscore tensor, no autograd graph for the loss)
+    def step_fused():
+        qg.grad = None
+        dg.grad = None
+        loss = maxsim_amd.score_contrastive_cross_entropy(qg, dg, off)
+        loss.backward()
+        return loss
+
+    for _ in range(W):
+        step_fused()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step_fused()
+    torch.cuda.synchronize()
+    ms_step_fused = (time.perf_counter() - t0) * 1e3 / K
+
     # kernel-level (op calls, no Python validation)
     ms_fwd = time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(q, d, off), K, 2)
     scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
@@ -476,6 +496,7 @@ def main():
     extra["c5"] = {
         "T_d": total, "flops_fwd": flops_fwd,
         "step_ms": round(ms_step, 4),
+        "fused_ce_step_ms": round(ms_step_fused, 4),
         "fwd_ms": round(ms_fwd, 4), "fwd_tflops": round(fwd_tflops, 2),
         "fwd_scoreonly_ms": round(ms_fwd_scoreonly, 4),
         "bwd_ms": round(ms_bwd, 4), "bwd_bytes": bytes_bwd,

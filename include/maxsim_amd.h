@@ -271,6 +271,50 @@ int maxsim_amd_contrastive_backward_typed(
     const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- Fused cross-entropy training loss ---------------------------------- */
+
+/* Loss reductions, numbered as torch's (none, mean, sum). */
+enum {
+  MAXSIM_REDUCTION_NONE = 0,
+  MAXSIM_REDUCTION_MEAN = 1,
+  MAXSIM_REDUCTION_SUM = 2
+};
+
+/* Cross-entropy over the rows of contrastive scores: the loss of the
+ * reference's training recipe, F.cross_entropy(scores / temperature,
+ * targets) after score_contrastive_train (README.md:193-205; the reference
+ * has no fused entry point, its users call torch).  scores [Nq, Nb] fp32
+ * (the forward's output), targets [Nq] int32 in [0, Nb) or NULL for the
+ * diagonal (target q = q, Nq <= Nb), inv_temperature = 1 / temperature.
+ * Writes lse [Nq] = logsumexp_b(scores[q, b] * inv_temperature), which the
+ * backward below needs, and loss: [Nq] per-row losses for
+ * MAXSIM_REDUCTION_NONE, else one value (mean or sum over rows, added in a
+ * fixed order).  An out-of-range target gives a NaN loss for its row. */
+int maxsim_amd_cross_entropy_forward(const float* scores, int64_t num_queries,
+                                     int64_t num_documents, const int32_t* targets,
+                                     float inv_temperature, int reduction, float* lse,
+                                     float* loss, void* stream);
+
+/* The contrastive backward of that loss, fused: the gradient of
+ * loss(score_contrastive(queries, documents)) with respect to queries and
+ * documents, where each score gradient
+ *   dscore[q, b] = w_q * (exp(scores[q, b] * inv_t - lse[q]) - [b == target_q]),
+ *   w_q = inv_t * grad_loss[q or 0] * (1 / Nq for MAXSIM_REDUCTION_MEAN),
+ * is computed inside the gradient kernels where they stage their weights:
+ * there is no dscore tensor and no separate softmax pass.  grad_loss is the
+ * upstream gradient of the loss ([Nq] for MAXSIM_REDUCTION_NONE, else one
+ * value, on the device).  Every other argument, the workspace and the
+ * gradient dtypes are those of maxsim_amd_contrastive_backward_typed.
+ * No counterpart in the reference, whose users run torch's cross-entropy
+ * and then maxsim_contrastive_backward on the resulting dscore. */
+int maxsim_amd_contrastive_ce_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* scores, const float* lse,
+    const int32_t* targets, const float* grad_loss, int reduction, float inv_temperature,
+    const void* queries, int64_t num_queries, int64_t Lq, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* ---- Padded -> packed --------------------------------------------------- */
 
 /* Replaces the boolean-mask gathers of `_pack_padded`

@@ -28,6 +28,7 @@ from maxsim_amd import (  # noqa: F401  (re-exported)
     score_candidates_padded_with_argmax_reference,
     score_contrastive,
     score_contrastive_backward_reference,
+    score_contrastive_cross_entropy,
     score_contrastive_reference,
     score_contrastive_train,
     score_contrastive_with_argmax,

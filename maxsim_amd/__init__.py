@@ -769,3 +769,90 @@ def score_contrastive_train(queries, documents, document_offsets) -> torch.Tenso
     return _checked_contrastive(
         queries, documents, document_offsets,
         lambda: _ContrastiveFn.apply(queries, documents, document_offsets))
+
+
+# ---------------------------------------------------------------------------
+# Fused contrastive cross-entropy (the training loss of the reference's README)
+# ---------------------------------------------------------------------------
+_REDUCTIONS = {"none": 0, "mean": 1, "sum": 2}
+
+
+class _ContrastiveCEFn(torch.autograd.Function):
+    """score_contrastive_train + F.cross_entropy(scores / temperature, targets)
+    in one autograd node: the forward writes the scores, their argmax and each
+    row's log-sum-exp; the backward computes the score gradients inside the
+    dQ/dD kernels from those (no dscore tensor, no separate softmax pass)."""
+
+    @staticmethod
+    def forward(ctx, queries, documents, document_offsets, targets, inv_t, reduction):
+        q, d = queries.contiguous(), documents.contiguous()
+        offs = document_offsets.to(torch.int32).contiguous()
+        scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, offs)
+        tgt = None if targets is None else targets.to(torch.int32).contiguous()
+        lse, loss = ops.maxsim_cross_entropy_forward(scores, tgt, inv_t, reduction)
+        if tgt is None:
+            ctx.save_for_backward(q, d, offs, argmax, scores, lse)
+        else:
+            ctx.save_for_backward(q, d, offs, argmax, scores, lse, tgt)
+        ctx.inv_t = inv_t
+        ctx.reduction = reduction
+        ctx.mark_non_differentiable(scores)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        saved = ctx.saved_tensors
+        q, d, offs, argmax, scores, lse = saved[:6]
+        tgt = saved[6] if len(saved) > 6 else None
+        dq, dd = ops.maxsim_contrastive_cross_entropy_backward(
+            grad_loss.contiguous().to(torch.float32), scores, lse, tgt, ctx.inv_t,
+            ctx.reduction, q, d, offs, argmax)
+        return dq, dd, None, None, None, None
+
+
+def score_contrastive_cross_entropy(queries, documents, document_offsets, targets=None, *,
+                                    temperature: float = 1.0,
+                                    reduction: str = "mean") -> torch.Tensor:
+    """The contrastive training loss in one call:
+    ``F.cross_entropy(score_contrastive_train(queries, documents,
+    document_offsets) / temperature, targets, reduction=reduction)``, the
+    recipe of the reference's README (README.md:193-205), with the softmax
+    gradient fused into the backward kernels.
+
+    Args:
+        queries, documents, document_offsets: as :func:`score_contrastive`.
+        targets: ``[Nq]`` int32/int64 class (document) per query, or None for
+            the diagonal (query i's positive is document i; needs Nq <= Nb).
+        temperature: the scores are divided by it (> 0).
+        reduction: ``"mean"`` (default), ``"sum"`` or ``"none"`` (``[Nq]``).
+
+    Returns:
+        fp32 loss (0-dim, or ``[Nq]`` for ``"none"``); differentiable with
+        respect to queries and documents (gradients in their dtype).  Not in
+        the reference's ``__all__``; its users call torch's cross-entropy.
+    """
+    _check_contrastive(queries, documents, document_offsets)
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"reduction must be 'mean', 'sum' or 'none'; got {reduction!r}")
+    temperature = float(temperature)
+    if not (temperature > 0.0 and np.isfinite(temperature)):
+        raise ValueError(f"temperature must be finite and > 0; got {temperature}")
+    Nq, Nb = queries.shape[0], document_offsets.numel() - 1
+    if targets is None:
+        if Nq > Nb:
+            raise ValueError(
+                f"diagonal targets need Nq <= Nb; got Nq={Nq}, Nb={Nb} (pass targets)")
+    else:
+        _require_index("targets", targets)
+        if targets.dim() != 1 or targets.shape[0] != Nq:
+            raise ValueError(f"targets must have shape [Nq={Nq}]; got {tuple(targets.shape)}")
+        _require_one_device(queries=queries, targets=targets)
+        t = _to_host(targets)[0]
+        bad = np.flatnonzero((t < 0) | (t >= Nb))
+        if bad.size:
+            i = int(bad[0])
+            raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {Nb})")
+    return _checked_contrastive(
+        queries, documents, document_offsets,
+        lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets,
+                                       1.0 / temperature, _REDUCTIONS[reduction]))

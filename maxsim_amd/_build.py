@@ -26,7 +26,7 @@ REPO = PKG.parent
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("MAXSIM_AMD_ARCH", "gfx950")
 
-HIP_SOURCES = ["maxsim_fwd.hip", "maxsim_bwd.hip", "maxsim_pack.hip", "maxsim_capi.hip"]
+HIP_SOURCES = ["maxsim_fwd.hip", "maxsim_bwd.hip", "maxsim_pack.hip", "maxsim_ce.hip", "maxsim_capi.hip"]
 LIB = PKG / "libmaxsim_amd.so"
 TORCH_LIB = PKG / "_maxsim_amd_torch.so"
 

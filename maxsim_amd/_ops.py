@@ -8,7 +8,10 @@ gfx950 behind the C ABI in ``include/maxsim_amd.h``.  Two more operators,
 are the contrastive and packed backwards with the gradients in the inputs'
 dtype; the autograd Functions use them so that torch does not cast fp32
 gradients in a separate pass.  ``maxsim_pack_padded_rows`` is the device
-copy behind :func:`maxsim_amd._pack_padded` (padded -> packed rows).
+copy behind :func:`maxsim_amd._pack_padded` (padded -> packed rows), and
+``maxsim_cross_entropy_forward`` / ``maxsim_contrastive_cross_entropy_backward``
+are the fused training loss behind
+:func:`maxsim_amd.score_contrastive_cross_entropy`.
 
 Importing this module loads ``_maxsim_amd_torch.so`` (which pulls in
 ``libmaxsim_amd.so``).  There is no fallback: if the native build is missing
@@ -123,6 +126,18 @@ def _(padded, lengths, offsets, max_len, packed_rows):
 
 @torch.library.register_fake("maxsim_amd::maxsim_contrastive_backward_typed")
 def _(dscore, queries, documents, document_offsets, argmax):
+    return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
+
+
+@torch.library.register_fake("maxsim_amd::maxsim_cross_entropy_forward")
+def _(scores, targets, inv_temperature, reduction):
+    nq = scores.shape[0]
+    return _f32(scores, (nq,)), _f32(scores, (nq,) if reduction == 0 else ())
+
+
+@torch.library.register_fake("maxsim_amd::maxsim_contrastive_cross_entropy_backward")
+def _(grad_loss, scores, lse, targets, inv_temperature, reduction, queries, documents,
+      document_offsets, argmax):
     return queries.new_empty(queries.shape), documents.new_empty(documents.shape)
 
 

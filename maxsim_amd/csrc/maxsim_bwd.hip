@@ -164,7 +164,35 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(E* p, int64_t n, bool ve
 // rows q*Lq .. and is scored against every document b; for padded, query b
 // has rows b*Lq_max .. and candidates p = b*C + c.
 // ---------------------------------------------------------------------------
+// Upstream gradient of the contrastive score (query q, document b).  With
+// `scores` null it is dscore[q * nb + b].  Otherwise the scores are the
+// logits of a cross-entropy over each query's row (the fused loss of
+// maxsim_amd_contrastive_ce_backward_typed): the gradient is
+//   w_q * (exp(s[q, b] * inv_t - lse_q) - [b == target_q]),
+//   w_q = scale * inv_t * grad_loss[per_row ? q : 0],
+// computed where the kernels stage their weights, so no dscore tensor is
+// written or read.
+struct CeGrad {
+  const float* scores = nullptr;
+  const float* lse = nullptr;
+  const int32_t* targets = nullptr;  // null: target_q = q (diagonal positives)
+  const float* grad_loss = nullptr;
+  int per_row = 0;
+  float inv_t = 1.0f;
+  float scale = 1.0f;
+};
+
+__device__ __forceinline__ float score_grad(const float* dscore, const CeGrad& ce, int64_t q,
+                                            int64_t b, int64_t nb) {
+  if (!ce.scores) return dscore[q * nb + b];
+  const float p = expf(ce.scores[q * nb + b] * ce.inv_t - ce.lse[q]);
+  const int64_t t = ce.targets ? (int64_t)ce.targets[q] : q;
+  const float w = ce.scale * ce.inv_t * ce.grad_loss[ce.per_row ? q : 0];
+  return w * (p - (b == t ? 1.0f : 0.0f));
+}
+
 struct DqArgs {
+  CeGrad ce;
   const float* dscore;
   const void* q;  // unused by the gather itself (kept for symmetry)
   const void* d;
@@ -211,7 +239,6 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
   constexpr int U = 8;
   if (!a.padded) {
     const int32_t* am = a.argmax + qidx * a.nb * a.lq + i;
-    const float* gq = a.dscore + qidx * a.nb;
     for (int64_t b0 = 0; b0 < a.nb; b0 += U) {
       int64_t src[U];
       float w[U];
@@ -236,7 +263,7 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t b = min(b0 + u, a.nb - 1);
-        const float gb = (w[u] != 0.0f) ? gq[b] : 0.0f;
+        const float gb = (w[u] != 0.0f) ? score_grad(a.dscore, a.ce, qidx, b, a.nb) : 0.0f;
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2)
           acc[e2] = (w[u] != 0.0f) ? fmaf(gb, v[u][e2], acc[e2]) : acc[e2];
@@ -359,7 +386,7 @@ __global__ __launch_bounds__(256) void dq_split_kernel(DqArgs a, bool vec, float
         const int j = a.argmax[(qidx * a.nb + b) * a.lq + i];
         if (s0 >= 0 && s1 > s0 && s1 <= a.total_d && j >= 0 && j < s1 - s0) {
           src = (int32_t)(s0 + j);
-          w = a.dscore[qidx * a.nb + b];
+          w = score_grad(a.dscore, a.ce, qidx, b, a.nb);
         }
       }
       t_src[e] = src;
@@ -485,7 +512,7 @@ __global__ __launch_bounds__(256) void dq_walk_kernel(DqArgs a, int rows_per_gro
         const int j = a.argmax[(qidx * a.nb + b) * a.lq + i];
         if (s0 >= 0 && s1 > s0 && s1 <= a.total_d && j >= 0 && j < s1 - s0) {
           src = OFF32 ? (int32_t)((uint32_t)(s0 + j) * row_bytes) : (int32_t)(s0 + j);
-          w = a.dscore[qidx * a.nb + b];
+          w = score_grad(a.dscore, a.ce, qidx, b, a.nb);
         }
       }
       t_src[r * stride + d] = src;
@@ -609,7 +636,7 @@ void dq_range_kernel(DqArgs a, float* __restrict__ ws) {
     for (int x = tid; x < nd * QW; x += 256) {
       const int d = x / QW;
       const int64_t q = q_first + (x - d * QW);
-      t_g[x] = q < a.rows / a.lq ? a.dscore[q * a.nb + c0 + d] : 0.0f;
+      t_g[x] = q < a.rows / a.lq ? score_grad(a.dscore, a.ce, q, c0 + d, a.nb) : 0.0f;
     }
     for (int x = tid; x <= nd; x += 256) t_off[x] = a.doff[c0 + x];
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies landed
@@ -732,6 +759,7 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict_
 // is repeated per part; its argmax reads are the cheaper side.
 // ---------------------------------------------------------------------------
 struct DdArgs {
+  CeGrad ce;
   const float* dscore;
   const void* q;
   const int32_t* argmax;
@@ -839,7 +867,8 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
         const int32_t* am_p = am_b + q0 * am_qstride + i0;
         const S* Qp = Q + (q0 * a.lq + i0) * (int64_t)a.dim;
         for (int x = tid; x <= nrows; x += kDdThreads) start[x] = 0;
-        for (int x = tid; x < qc; x += kDdThreads) gst[x] = a.dscore[(q0 + x) * a.nb + b];
+        for (int x = tid; x < qc; x += kDdThreads)
+          gst[x] = score_grad(a.dscore, a.ce, q0 + x, b, a.nb);
         __syncthreads();
         // Entry x's target row, relative to the row pass (out of range: not
         // in this pass or invalid).  Both sort phases read the argmax
@@ -1065,7 +1094,7 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
   const uint32_t off_t = (uint32_t)(q_t * am_qstride + i_t) * 4u;
   const uint32_t off_step = (uint32_t)(q_step * am_qstride) * 4u;
   const uint32_t off_last = (uint32_t)((a.nq - 1) * am_qstride + (a.lq - 1)) * 4u;
-  for (int x = tid; x < a.nq; x += kDdThreads) gst[x] = a.dscore[x * a.nb + b];
+  for (int x = tid; x < a.nq; x += kDdThreads) gst[x] = score_grad(a.dscore, a.ce, x, b, a.nb);
 
   // entries of this thread with a valid query: k < nk
   const int nk_t = min((int)((a.nq - q_t + q_step - 1) / q_step), kBkMaxEntriesPerThread);
@@ -1164,15 +1193,27 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
                 f[k][u].hi = load16(Qb, o + 16u);
               }
             }
+          // past the bucket's end (the last step of a block) an entry
+          // repeats the step's first one; its fragment and weight are zeroed
+          // (fmaf(0, 0, x) == x exactly), which is cheaper than selecting
+          // each of its sums
+          if constexpr (MASKED) {
+#pragma unroll
+            for (int k = 0; k < kBkBatch; ++k) {
+              if (!ok[k]) {
+                gx[k] = 0.0f;
+#pragma unroll
+                for (int u = 0; u < NS; ++u) f[k][u] = zero_frag<T>();
+              }
+            }
+          }
 #pragma unroll
           for (int k = 0; k < kBkBatch; ++k)
 #pragma unroll
             for (int u = 0; u < NS; ++u)
 #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const float t = fmaf(gx[k], frag_elem(f[k][u], e), blk[u][e]);
-                blk[u][e] = (!MASKED || ok[k]) ? t : blk[u][e];
-              }
+              for (int e = 0; e < 8; ++e)
+                blk[u][e] = fmaf(gx[k], frag_elem(f[k][u], e), blk[u][e]);
         };
         int s = s0;
         for (; s + kBkBatch <= s1; s += kBkBatch) batch(s, std::false_type{});
@@ -2472,26 +2513,12 @@ static int packed_backward_impl(
   return check_launch("dq_packed_kernel / dd_packed_kernel");
 }
 
-}  // namespace maxsim
-
-using namespace maxsim;
-
-extern "C" {
-
-size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
-                                                      int64_t dim) {
-  // the split pass keeps a workgroup's rows x slices within 256 threads
-  if (num_queries <= 0 || Lq <= 0 || dim <= 0 || dim > kDqSplitMaxDim) return 0;
-  return (size_t)kXcds * (size_t)num_queries * (size_t)Lq * (size_t)dim * sizeof(float);
-}
-
-int maxsim_amd_contrastive_backward_typed(
-    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
-    int64_t num_queries, int64_t Lq, const void* documents, int64_t total_d_tokens,
-    const int32_t* document_offsets, int64_t num_documents, const int32_t* argmax,
-    int64_t dim, void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
-    void* stream) {
-  clear_error();
+static int contrastive_backward_impl(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const CeGrad& ce,
+    const void* queries, int64_t num_queries, int64_t Lq, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (int e = check_dtype(dtype)) return e;
   if (grad_dtype != MAXSIM_FLOAT32 && grad_dtype != dtype)
     return fail(MAXSIM_ERR_INVALID, "grad_dtype must be MAXSIM_FLOAT32 or the input dtype");
@@ -2513,7 +2540,7 @@ int maxsim_amd_contrastive_backward_typed(
     if (total_d_tokens > 0) launch_fill_grad(ddocuments, total_d_tokens * dim, out16, st);
     return check_launch("fill_zero_kernel");
   }
-  if (!dscore || !queries || !documents || !document_offsets || !argmax)
+  if ((!dscore && !ce.scores) || !queries || !documents || !document_offsets || !argmax)
     return fail(MAXSIM_ERR_INVALID, "null pointer argument");
   if (total_d_tokens <= 0)
     return fail(MAXSIM_ERR_INVALID, "documents must not be empty when Nb > 0");
@@ -2523,6 +2550,7 @@ int maxsim_amd_contrastive_backward_typed(
   // ids; use up to 80 KB when the device allows, so C5-sized batches
   // (Nq * Lq = 16384 entries) need a single pass.
   DdArgs da{};
+  da.ce = ce;
   da.dscore = dscore;
   da.q = queries;
   da.argmax = argmax;
@@ -2570,6 +2598,7 @@ int maxsim_amd_contrastive_backward_typed(
 
   // dq
   DqArgs qa{};
+  qa.ce = ce;
   qa.dscore = dscore;
   qa.q = queries;
   qa.d = documents;
@@ -2633,6 +2662,66 @@ int maxsim_amd_contrastive_backward_typed(
   }
   MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, out16, st);
   return check_launch("dd_contrastive_kernel");
+}
+
+}  // namespace maxsim
+
+using namespace maxsim;
+
+extern "C" {
+
+size_t maxsim_amd_contrastive_backward_workspace_size(int64_t num_queries, int64_t Lq,
+                                                      int64_t dim) {
+  // the split pass keeps a workgroup's rows x slices within 256 threads
+  if (num_queries <= 0 || Lq <= 0 || dim <= 0 || dim > kDqSplitMaxDim) return 0;
+  return (size_t)kXcds * (size_t)num_queries * (size_t)Lq * (size_t)dim * sizeof(float);
+}
+
+int maxsim_amd_contrastive_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore, const void* queries,
+    int64_t num_queries, int64_t Lq, const void* documents, int64_t total_d_tokens,
+    const int32_t* document_offsets, int64_t num_documents, const int32_t* argmax,
+    int64_t dim, void* dqueries, void* ddocuments, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  clear_error();
+  if (!dscore && num_queries > 0 && num_documents > 0)
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  return contrastive_backward_impl(dtype, grad_dtype, dscore, CeGrad{}, queries, num_queries, Lq,
+                                   documents, total_d_tokens, document_offsets, num_documents,
+                                   argmax, dim, dqueries, ddocuments, workspace, workspace_bytes,
+                                   stream);
+}
+
+int maxsim_amd_contrastive_ce_backward_typed(
+    maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* scores, const float* lse,
+    const int32_t* targets, const float* grad_loss, int reduction, float inv_temperature,
+    const void* queries, int64_t num_queries, int64_t Lq, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets, int64_t num_documents,
+    const int32_t* argmax, int64_t dim, void* dqueries, void* ddocuments, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (reduction < MAXSIM_REDUCTION_NONE || reduction > MAXSIM_REDUCTION_SUM)
+    return fail(MAXSIM_ERR_INVALID, "unknown reduction %d", reduction);
+  if (!(inv_temperature > 0.0f) || !(inv_temperature < INFINITY))
+    return fail(MAXSIM_ERR_INVALID, "inv_temperature must be finite and > 0");
+  if (num_queries > 0 && num_documents > 0 && (!scores || !lse || !grad_loss))
+    return fail(MAXSIM_ERR_INVALID, "null pointer argument");
+  if (!targets && num_queries > num_documents)
+    return fail(MAXSIM_ERR_INVALID,
+                "diagonal targets (targets == NULL) need num_queries <= num_documents");
+  CeGrad ce;
+  ce.scores = scores;
+  ce.lse = lse;
+  ce.targets = targets;
+  ce.grad_loss = grad_loss;
+  ce.per_row = reduction == MAXSIM_REDUCTION_NONE ? 1 : 0;
+  ce.inv_t = inv_temperature;
+  ce.scale = (reduction == MAXSIM_REDUCTION_MEAN && num_queries > 0) ? 1.0f / (float)num_queries
+                                                                     : 1.0f;
+  return contrastive_backward_impl(dtype, grad_dtype, nullptr, ce, queries, num_queries, Lq,
+                                   documents, total_d_tokens, document_offsets, num_documents,
+                                   argmax, dim, dqueries, ddocuments, workspace, workspace_bytes,
+                                   stream);
 }
 
 int maxsim_amd_contrastive_backward(

@@ -12,6 +12,7 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
+#include <optional>
 #include <tuple>
 #include <vector>
 
@@ -412,21 +413,36 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_forward_with_argmax(
   return {scores, argmax};
 }
 
+// The fused cross-entropy's saved state: the score gradients are computed
+// from these inside the backward kernels instead of being read from dscore.
+struct CeSpec {
+  Tensor scores, lse, targets, grad_loss;  // targets undefined: the diagonal
+  int64_t reduction;
+  double inv_t;
+};
+
 // grads_in_input_dtype: write the gradients in the inputs' dtype (the C ABI's
 // typed entry point, rounding to nearest even like a cast); when the shapes
-// need the fp32 path, compute in fp32 and cast.
+// need the fp32 path, compute in fp32 and cast.  With `ce` the score
+// gradients come from the fused cross-entropy and `dscore` is unused.
 std::tuple<Tensor, Tensor> contrastive_backward_impl(
     Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
-    Tensor argmax, bool grads_in_input_dtype) {
+    Tensor argmax, bool grads_in_input_dtype, const CeSpec* ce = nullptr) {
   Contrastive c = prep_contrastive(queries, documents, document_offsets);
   const int64_t Nq = c.q.size(0), Lq = c.q.size(1), Nb = c.off.numel() - 1;
-  TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
   TORCH_CHECK(argmax.scalar_type() == at::kInt, "argmax must be int32");
-  check_on(dscore, c.q, "dscore");
   check_on(argmax, c.q, "argmax");
-  TORCH_CHECK(dscore.numel() == Nq * Nb, "dscore must be [Nq, Nb]");
   TORCH_CHECK(argmax.numel() == Nq * Nb * Lq, "argmax must be [Nq, Nb, Lq]");
-  Tensor g = dscore.contiguous();
+  Tensor g;
+  if (!ce) {
+    TORCH_CHECK(dscore.scalar_type() == at::kFloat, "dscore must be float32");
+    check_on(dscore, c.q, "dscore");
+    TORCH_CHECK(dscore.numel() == Nq * Nb, "dscore must be [Nq, Nb]");
+    g = dscore.contiguous();
+  } else {
+    TORCH_CHECK(ce->scores.numel() == Nq * Nb, "scores must be [Nq, Nb]");
+    TORCH_CHECK(ce->lse.numel() == Nq, "lse must be [Nq]");
+  }
   Tensor am = argmax.contiguous();
   c10::hip::HIPGuardMasqueradingAsCUDA guard(c.q.device());
   // With at least one document per XCD range, gather dq by range into a
@@ -442,11 +458,20 @@ std::tuple<Tensor, Tensor> contrastive_backward_impl(
   auto run = [&](maxsim_dtype grad_dt, const at::TensorOptions& opts) {
     Tensor dq = at::empty({Nq, Lq, c.q.size(2)}, opts);
     Tensor dd = at::empty({c.d.size(0), c.d.size(1)}, opts);
-    const int rc = maxsim_amd_contrastive_backward_typed(
-        dt, grad_dt, g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(), c.d.size(0),
-        c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(), c.q.size(2), dq.data_ptr(),
-        dd.data_ptr(), ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws_bytes : 0,
-        current_stream(c.q));
+    void* wsp = ws.defined() ? ws.data_ptr() : nullptr;
+    const size_t wsb = ws.defined() ? ws_bytes : 0;
+    const int rc =
+        ce ? maxsim_amd_contrastive_ce_backward_typed(
+                 dt, grad_dt, ce->scores.data_ptr<float>(), ce->lse.data_ptr<float>(),
+                 ce->targets.defined() ? ce->targets.data_ptr<int32_t>() : nullptr,
+                 ce->grad_loss.data_ptr<float>(), (int)ce->reduction, (float)ce->inv_t,
+                 c.q.data_ptr(), Nq, Lq, c.d.data_ptr(), c.d.size(0), c.off.data_ptr<int32_t>(),
+                 Nb, am.data_ptr<int32_t>(), c.q.size(2), dq.data_ptr(), dd.data_ptr(), wsp, wsb,
+                 current_stream(c.q))
+           : maxsim_amd_contrastive_backward_typed(
+                 dt, grad_dt, g.data_ptr<float>(), c.q.data_ptr(), Nq, Lq, c.d.data_ptr(),
+                 c.d.size(0), c.off.data_ptr<int32_t>(), Nb, am.data_ptr<int32_t>(),
+                 c.q.size(2), dq.data_ptr(), dd.data_ptr(), wsp, wsb, current_stream(c.q));
     return std::make_tuple(rc, dq, dd);
   };
   if (grads_in_input_dtype && dt != MAXSIM_FLOAT32) {
@@ -474,6 +499,67 @@ std::tuple<Tensor, Tensor> maxsim_contrastive_backward_typed(
     Tensor dscore, Tensor queries, Tensor documents, Tensor document_offsets,
     Tensor argmax) {
   return contrastive_backward_impl(dscore, queries, documents, document_offsets, argmax, true);
+}
+
+// ---- fused cross-entropy ----------------------------------------------------
+
+Tensor ce_targets(const std::optional<Tensor>& targets, const Tensor& scores) {
+  if (!targets.has_value()) return Tensor();
+  check_on(*targets, scores, "targets");
+  TORCH_CHECK(targets->dim() == 1 && targets->size(0) == scores.size(0),
+              "targets must be [Nq] (one class index per query row)");
+  return as_i32(*targets);
+}
+
+// Not one of the reference's operators: the loss of the reference's
+// training recipe, F.cross_entropy(scores * inv_temperature, targets)
+// (README.md:193-205), with the row log-sum-exp the fused backward needs.
+// reduction: 0 none ([Nq] loss), 1 mean, 2 sum (0-dim loss).
+std::tuple<Tensor, Tensor> maxsim_cross_entropy_forward(Tensor scores,
+                                                        std::optional<Tensor> targets,
+                                                        double inv_temperature,
+                                                        int64_t reduction) {
+  TORCH_CHECK(scores.device().is_cuda(), "scores must be a HIP (torch 'cuda') tensor");
+  TORCH_CHECK(scores.dim() == 2 && scores.scalar_type() == at::kFloat,
+              "scores must be float32 [Nq, Nb]");
+  Tensor s = scores.contiguous();
+  const int64_t nq = s.size(0), nb = s.size(1);
+  Tensor t = ce_targets(targets, s);
+  Tensor lse = at::empty({nq}, f32_opts(s));
+  Tensor loss = reduction == MAXSIM_REDUCTION_NONE ? at::empty({nq}, f32_opts(s))
+                                                   : at::empty({}, f32_opts(s));
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(s.device());
+  check_status(maxsim_amd_cross_entropy_forward(
+      s.data_ptr<float>(), nq, nb, t.defined() ? t.data_ptr<int32_t>() : nullptr,
+      (float)inv_temperature, (int)reduction, lse.data_ptr<float>(), loss.data_ptr<float>(),
+      current_stream(s)));
+  return {lse, loss};
+}
+
+// Not one of the reference's operators: the fused backward of that loss
+// through the contrastive scores, gradients in the inputs' dtype.
+std::tuple<Tensor, Tensor> maxsim_contrastive_cross_entropy_backward(
+    Tensor grad_loss, Tensor scores, Tensor lse, std::optional<Tensor> targets,
+    double inv_temperature, int64_t reduction, Tensor queries, Tensor documents,
+    Tensor document_offsets, Tensor argmax) {
+  check_on(scores, queries, "scores");
+  check_on(lse, queries, "lse");
+  check_on(grad_loss, queries, "grad_loss");
+  TORCH_CHECK(scores.scalar_type() == at::kFloat && lse.scalar_type() == at::kFloat &&
+                  grad_loss.scalar_type() == at::kFloat,
+              "scores, lse and grad_loss must be float32");
+  CeSpec ce;
+  ce.scores = scores.contiguous();
+  ce.lse = lse.contiguous();
+  ce.targets = ce_targets(targets, ce.scores);
+  ce.grad_loss = grad_loss.contiguous();
+  ce.reduction = reduction;
+  ce.inv_t = inv_temperature;
+  TORCH_CHECK(ce.grad_loss.numel() ==
+                  (reduction == MAXSIM_REDUCTION_NONE ? ce.scores.size(0) : 1),
+              "grad_loss must hold one value per row for reduction none, else one value");
+  return contrastive_backward_impl(Tensor(), queries, documents, document_offsets, argmax, true,
+                                   &ce);
 }
 
 // ---- padded -> packed -------------------------------------------------------
@@ -542,6 +628,11 @@ TORCH_LIBRARY(maxsim_amd, m) {
         "int packed_rows) -> Tensor");
   m.def("maxsim_contrastive_backward_typed(Tensor dscore, Tensor queries, Tensor documents, "
         "Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
+  m.def("maxsim_cross_entropy_forward(Tensor scores, Tensor? targets, float inv_temperature, "
+        "int reduction) -> (Tensor, Tensor)");
+  m.def("maxsim_contrastive_cross_entropy_backward(Tensor grad_loss, Tensor scores, "
+        "Tensor lse, Tensor? targets, float inv_temperature, int reduction, Tensor queries, "
+        "Tensor documents, Tensor document_offsets, Tensor argmax) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
@@ -559,4 +650,7 @@ TORCH_LIBRARY_IMPL(maxsim_amd, CUDA, m) {
   m.impl("maxsim_contrastive_backward", &maxsim_contrastive_backward);
   m.impl("maxsim_contrastive_backward_typed", &maxsim_contrastive_backward_typed);
   m.impl("maxsim_pack_padded_rows", &maxsim_pack_padded_rows);
+  m.impl("maxsim_cross_entropy_forward", &maxsim_cross_entropy_forward);
+  m.impl("maxsim_contrastive_cross_entropy_backward",
+         &maxsim_contrastive_cross_entropy_backward);
 }

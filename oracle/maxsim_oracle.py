@@ -44,6 +44,7 @@ __all__ = [
     "padded_backward",
     "packed_backward",
     "pack_padded",
+    "cross_entropy",
 ]
 
 
@@ -226,3 +227,25 @@ def pack_padded(queries, documents, query_lengths, doc_lengths):
     do = np.concatenate([[0], np.cumsum(dl.reshape(-1))]).astype(np.int64)
     pairs = np.arange(B * C, dtype=np.int64)
     return qp, qo, dp, do, pairs // max(C, 1), pairs, int(ql.max()) if B else 0
+
+
+def cross_entropy(scores, targets=None, inv_temperature=1.0, reduction="mean"):
+    """The loss of the reference's training recipe, F.cross_entropy(scores /
+    temperature, targets) (README.md:193-205), and its gradient with respect
+    to the scores: ``(loss, dscore)`` in float64, with ``targets`` None for
+    the diagonal.  dscore[q, b] = w_q * (softmax(s * inv_t)[q, b] - [b == t_q])
+    * inv_t, w_q = 1 / Nq (mean), 1 (sum) or the row's upstream 1 (none,
+    where the loss is per row and dscore is for a sum of the row losses)."""
+    s = _as64(scores) * float(inv_temperature)
+    Nq, Nb = s.shape
+    t = np.arange(Nq) if targets is None else np.asarray(targets, dtype=np.int64)
+    m = s.max(axis=1, keepdims=True)
+    lse = (m + np.log(np.exp(s - m).sum(axis=1, keepdims=True)))[:, 0]
+    rows = lse - s[np.arange(Nq), t]
+    p = np.exp(s - lse[:, None])
+    onehot = np.zeros_like(p)
+    onehot[np.arange(Nq), t] = 1.0
+    w = 1.0 / Nq if reduction == "mean" else 1.0
+    dscore = (p - onehot) * (w * float(inv_temperature))
+    loss = rows if reduction == "none" else (rows.mean() if reduction == "mean" else rows.sum())
+    return loss, dscore

@@ -228,3 +228,24 @@ def test_cpu_tensors_never_fall_back():
     q, d, cu = _contrastive()
     with pytest.raises(NotImplementedError):
         maxsim_amd.score_contrastive(q, d, cu)
+
+
+def test_cross_entropy_validation():
+    """score_contrastive_cross_entropy rejects bad reductions, temperatures
+    and targets before anything runs (CPU tensors: the checks come first)."""
+    q, d, off = _contrastive(Nq=3, Nb=4)
+    with pytest.raises(ValueError, match="reduction"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, reduction="avg")
+    with pytest.raises(ValueError, match="temperature"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, temperature=0.0)
+    with pytest.raises(ValueError, match="temperature"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, temperature=float("nan"))
+    with pytest.raises(ValueError, match="targets"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, torch.tensor([0, 1]))
+    with pytest.raises(ValueError, match="out of range"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, torch.tensor([0, 1, 4]))
+    with pytest.raises(TypeError, match="int32 or int64"):
+        maxsim_amd.score_contrastive_cross_entropy(q, d, off, torch.tensor([0.0, 1.0, 2.0]))
+    q5, d5, off5 = _contrastive(Nq=5, Nb=4)
+    with pytest.raises(ValueError, match="diagonal"):
+        maxsim_amd.score_contrastive_cross_entropy(q5, d5, off5)

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 18, names
+    assert len(names) == 20, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 8
+    assert lib.maxsim_amd_abi_version() == 9
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -213,3 +213,32 @@ def test_pack_rejects_bad_arguments(lib):
     assert fn(F32, None, 0, 4, None, None, 8, None, 0, None) == OK
     # more padded bytes per segment than one launch covers
     assert fn(F32, one, 2, 1 << 28, one, one, 256, one, 8, None) == UNSUPPORTED
+
+
+def test_cross_entropy_entry_points_reject_bad_arguments(lib):
+    """The fused loss's forward and backward check their arguments before
+    touching the device."""
+    fwd = lib.maxsim_amd_cross_entropy_forward
+    fwd.argtypes = [P, I64, I64, P, ctypes.c_float, ctypes.c_int, P, P, P]
+    one = P(16)
+    assert fwd(one, 4, 8, None, 1.0, 3, one, one, None) == INVALID      # reduction
+    assert b"reduction" in lib.maxsim_amd_last_error()
+    assert fwd(one, 4, 8, None, 0.0, 1, one, one, None) == INVALID      # temperature
+    assert fwd(one, 4, 8, None, float("inf"), 1, one, one, None) == INVALID
+    assert fwd(one, 9, 8, None, 1.0, 1, one, one, None) == INVALID      # diagonal needs Nq <= Nb
+    assert b"diagonal" in lib.maxsim_amd_last_error()
+    assert fwd(one, -1, 8, None, 1.0, 1, one, one, None) == INVALID
+    assert fwd(None, 4, 8, None, 1.0, 1, one, one, None) == INVALID
+    bwd = lib.maxsim_amd_contrastive_ce_backward_typed
+    bwd.argtypes = [ctypes.c_int, ctypes.c_int, P, P, P, P, ctypes.c_int, ctypes.c_float,
+                    P, I64, I64, P, I64, P, I64, P, I64, P, P, P, ctypes.c_size_t, P]
+    args = [BF16, BF16, one, one, None, one, 1, 1.0, one, 2, 16, one, 64, one, 2, one, 64,
+            one, one, None, 0, None]
+    bad = list(args); bad[6] = 5
+    assert bwd(*bad) == INVALID
+    bad = list(args); bad[7] = -1.0
+    assert bwd(*bad) == INVALID
+    bad = list(args); bad[2] = None
+    assert bwd(*bad) == INVALID
+    bad = list(args); bad[9] = 3                                           # Nq > Nb, diagonal
+    assert bwd(*bad) == INVALID

@@ -317,3 +317,36 @@ def test_pack_padded_mutant_is_caught(monkeypatch, mutant):
     monkeypatch.setattr(oracle, "pack_padded", broken)
     with pytest.raises(AssertionError):
         pin_pack_padded()
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("with_targets", [False, True])
+def test_cross_entropy_matches_torch(reduction, with_targets):
+    """oracle.cross_entropy is F.cross_entropy(scores / T, targets) and its
+    autograd gradient (the library routine the reference's README calls)."""
+    gen = torch.Generator().manual_seed(11)
+    s = torch.randn(6, 9, generator=gen, dtype=torch.float64) * 5
+    t = torch.randint(0, 9, (6,), generator=gen) if with_targets else None
+    inv_t = 1 / 0.3
+    sr = s.clone().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(sr * inv_t, t if t is not None else torch.arange(6),
+                                            reduction=reduction)
+    ref.backward(torch.ones_like(ref))
+    loss, dscore = oracle.cross_entropy(s.numpy(), None if t is None else t.numpy(), inv_t,
+                                        reduction)
+    np.testing.assert_allclose(loss, ref.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dscore, sr.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_cross_entropy_catches_planted_mistakes():
+    """A softmax without the max shift overflows, a dropped temperature or a
+    wrong target both change the gradient: the torch pin above would fail."""
+    s = np.array([[1000.0, 999.0, 0.0], [0.0, 1.0, 2.0]])
+    loss, dscore = oracle.cross_entropy(s, None, 1.0, "mean")
+    assert np.isfinite(loss) and np.all(np.isfinite(dscore))
+    # rows of the gradient sum to zero (softmax sums to one)
+    np.testing.assert_allclose(dscore.sum(axis=1), 0.0, atol=1e-12)
+    _, d2 = oracle.cross_entropy(s, None, 0.5, "mean")
+    assert not np.allclose(dscore, d2)
+    _, d3 = oracle.cross_entropy(s, np.array([1, 1]), 1.0, "mean")
+    assert not np.allclose(dscore, d3)
