@@ -17,6 +17,7 @@ from maxsim_amd import (  # noqa: F401  (re-exported)
     __all__,
     __version__,
     _pack_padded,
+    host_checks,
     maxsim_reference,
     maxsim_reference_with_argmax,
     pack_documents,
@@ -39,6 +40,7 @@ from maxsim_amd import (  # noqa: F401  (re-exported)
     score_pairs_packed_train,
     score_pairs_packed_with_argmax,
     score_pairs_packed_with_argmax_reference,
+    set_host_checks,
 )
 
 from . import _ops, reference  # noqa: F401,E402

@@ -25,6 +25,8 @@ they are never used by the operators.
 
 from __future__ import annotations
 
+import contextlib
+import os
 from typing import Tuple
 
 import numpy as np
@@ -69,6 +71,55 @@ __all__ = [
 
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 _INDEXES = (torch.int32, torch.int64)
+
+
+# ---------------------------------------------------------------------------
+# Host checks of device data (offsets, ids, lengths, targets)
+# ---------------------------------------------------------------------------
+_HOST_CHECKS = os.environ.get("MAXSIM_AMD_HOST_CHECKS", "1") != "0"
+
+
+def set_host_checks(enabled: bool) -> bool:
+    """Turn the host-side checks of device-resident layout data on (the
+    default) or off, process-wide; returns the previous setting.  The
+    environment variable ``MAXSIM_AMD_HOST_CHECKS=0`` sets it off at import.
+
+    On, every call copies its offsets / ids / lengths to the host and raises
+    the reference's errors for invalid values, which makes the host wait for
+    that copy once per call (overlapped with the kernels, but a wait).
+
+    Off, a call on device tensors never waits for the device: only the checks
+    that need no device data run (shapes, dtypes, devices), and the kernels'
+    own handling of invalid layouts is the contract:
+
+    * a contrastive document with an invalid range (end <= start, start < 0,
+      end beyond the documents), a packed pair with an out-of-range id, an
+      invalid segment or a query longer than ``max_q_len``, a padded
+      candidate or query with a length outside ``(0, padded extent]``: NaN
+      score (argmax 0), no gradient from it, nothing read out of range;
+    * a cross-entropy target outside ``[0, Nb)``: NaN loss for its row;
+    * offsets that are valid ranges but break the CSR convention (not
+      starting at 0, not ending at the row count, overlapping) are scored as
+      they say; gradient rows that no valid segment covers are unspecified.
+
+    The packed ``_with_argmax`` / ``_train`` functions size the argmax by the
+    longest query: without ``max_q_len`` they still read that one integer
+    back.  Everything else is capturable in a HIP graph with checks off."""
+    global _HOST_CHECKS
+    previous = _HOST_CHECKS
+    _HOST_CHECKS = bool(enabled)
+    return previous
+
+
+@contextlib.contextmanager
+def host_checks(enabled: bool):
+    """Context manager form of :func:`set_host_checks` (process-wide while
+    the block runs)."""
+    previous = set_host_checks(enabled)
+    try:
+        yield
+    finally:
+        set_host_checks(previous)
 
 
 # ---------------------------------------------------------------------------
@@ -208,6 +259,8 @@ def _checked_padded(queries, documents, query_lengths, doc_lengths, launch):
     work queued before a failing check is harmless and its result is
     dropped."""
     B, C, Lq, Ld, _ = _check_padded_meta(queries, documents, query_lengths, doc_lengths)
+    if not _HOST_CHECKS and query_lengths.is_cuda:
+        return launch(B, C, Lq, Ld)
     if not query_lengths.is_cuda:  # host tensors: check first (the operators reject them anyway)
         qlen, dlen = _to_host(query_lengths, doc_lengths)
         _check_lengths(qlen, Lq, "query_lengths")
@@ -306,6 +359,14 @@ def _checked_packed(queries, query_offsets, documents, document_offsets,
             pair_query_ids, pair_document_ids)))
     if max_q_len is not None and max_q_len <= 0:
         raise ValueError(f"max_q_len must be > 0; got {max_q_len}")
+    if not _HOST_CHECKS:
+        if max_q_len is not None:
+            return launch(int(max_q_len))
+        if not shape_needs_max:
+            return launch(max(int(queries.shape[0]), 1))
+        mql = _device_max_segment(query_offsets, int(queries.shape[0]))
+        # offsets that cannot be well formed: every pair is invalid anyway
+        return launch(mql if mql is not None else 1)
     # queued before the read-back below, so that only the launch sits
     # between the host's wait for the longest query and the kernels
     hosts, copied = _host_copies_async(query_offsets, document_offsets, pair_query_ids,
@@ -699,6 +760,10 @@ def _checked_contrastive(queries, documents, document_offsets, launch):
     NaN, nothing is read out of range) and their results are dropped."""
     _check_contrastive(queries, documents, document_offsets)
     flat = document_offsets.detach().reshape(-1)
+    if not _HOST_CHECKS and flat.is_cuda:
+        if documents.shape[0] == 0:
+            raise ValueError("documents must not be empty (document_offsets has >= 1 document)")
+        return launch()
     if not flat.is_cuda:  # host tensors: check first (the operators reject them anyway)
         _check_offsets(flat.numpy().astype(np.int64), documents.shape[0])
         return launch()
@@ -847,11 +912,12 @@ def score_contrastive_cross_entropy(queries, documents, document_offsets, target
         if targets.dim() != 1 or targets.shape[0] != Nq:
             raise ValueError(f"targets must have shape [Nq={Nq}]; got {tuple(targets.shape)}")
         _require_one_device(queries=queries, targets=targets)
-        t = _to_host(targets)[0]
-        bad = np.flatnonzero((t < 0) | (t >= Nb))
-        if bad.size:
-            i = int(bad[0])
-            raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {Nb})")
+        if _HOST_CHECKS or not targets.is_cuda:
+            t = _to_host(targets)[0]
+            bad = np.flatnonzero((t < 0) | (t >= Nb))
+            if bad.size:
+                i = int(bad[0])
+                raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {Nb})")
     return _checked_contrastive(
         queries, documents, document_offsets,
         lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets,

@@ -753,10 +753,11 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict_
 // rows already written).
 //
 // Every document gathers rows from all of Q, so Q should stay in L2.  The
-// embedding dimension is split into `parts` (1, 2 or 4) slice ranges, part p
-// handled only by XCDs [p * 8 / parts, (p + 1) * 8 / parts) (workgroup w runs
-// on XCD w % 8): each XCD then gathers from 1 / parts of Q.  The bucketing
-// is repeated per part; its argmax reads are the cheaper side.
+// embedding dimension is split into `parts` (1, 2, 4 or 8) slice ranges, part
+// p handled only by XCDs [p * 8 / parts, (p + 1) * 8 / parts) (workgroup w
+// runs on XCD w % 8): each XCD then gathers from 1 / parts of Q.  The
+// bucketing is repeated per part; its argmax reads are the cheaper side.
+// Batches of few documents also take more parts, to fill the chip.
 // ---------------------------------------------------------------------------
 struct DdArgs {
   CeGrad ce;
@@ -773,7 +774,7 @@ struct DdArgs {
   int nslices;
   int rows_per_pass;     // R: rows bucketed per pass (LDS: 2 * (R + 1) ints)
   int entries_per_pass;  // E: entry ids held per pass (LDS: E ints)
-  int parts;             // dimension parts (1, 2 or 4; divides kXcds)
+  int parts;             // dimension parts (1, 2, 4 or 8; divides kXcds)
   int part_slices;       // 8-element slices per part (last part may hold fewer)
   int group;             // lanes per row: power of two, <= 16, part_slices <= NS * group
 };
@@ -2640,15 +2641,23 @@ static int contrastive_backward_impl(
   // thread, and parts of exactly 2 * G slices with G a power of two <= 16
   {
     const int64_t ne_all = num_queries * Lq;
-    const int g2 = da.part_slices;  // one slice per lane
+    // Few documents: more dimension parts (up to one per XCD), so that the
+    // launch has about two workgroups per CU; each part buckets its
+    // document's entries again, which costs little at such sizes.
+    int parts = da.parts;
+    while (parts < kXcds && num_documents * parts < 512 && nslices % (parts * 2) == 0)
+      parts *= 2;
+    const int g2 = nslices / parts;  // one slice per lane
     const bool bucket = vec && kDdThreads % Lq == 0 && g2 >= 1 &&
                         g2 <= kDdMaxGroup &&
-                        (g2 & (g2 - 1)) == 0 && da.part_slices * da.parts == nslices &&
+                        (g2 & (g2 - 1)) == 0 && g2 * parts == nslices &&
                         ne_all <= (int64_t)kDdThreads * kBkMaxEntriesPerThread &&
                         q_bytes < ((int64_t)1 << 31) &&
                         num_queries * num_documents * Lq < ((int64_t)1 << 31);
     if (bucket) {
       DdArgs ba = da;
+      ba.parts = parts;
+      ba.part_slices = g2;
       ba.group = g2;
       ba.rows_per_pass = 1024;
       ba.entries_per_pass = (int)ne_all;

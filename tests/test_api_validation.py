@@ -249,3 +249,30 @@ def test_cross_entropy_validation():
     q5, d5, off5 = _contrastive(Nq=5, Nb=4)
     with pytest.raises(ValueError, match="diagonal"):
         maxsim_amd.score_contrastive_cross_entropy(q5, d5, off5)
+
+
+def test_host_checks_switch():
+    """set_host_checks / host_checks toggle the process-wide setting and
+    restore it; with checks off, shape and dtype errors still raise, and
+    layout data on the host is still checked (only device-resident data is
+    left to the kernels)."""
+    assert maxsim_amd.set_host_checks(False) is True
+    try:
+        q, d, _ = _contrastive()
+        with pytest.raises(ValueError, match="Lq"):
+            maxsim_amd.score_contrastive(q[:, :0], d, torch.tensor([0, 8], dtype=torch.int32))
+        with pytest.raises(ValueError, match="0|start|offset"):
+            maxsim_amd.score_contrastive(q, d, torch.tensor([1, 33, 65, 97, 129],
+                                                            dtype=torch.int32))
+        with pytest.raises(TypeError, match="int32 or int64"):
+            maxsim_amd.score_contrastive(q, d, torch.tensor([0.0, 8.0]))
+    finally:
+        assert maxsim_amd.set_host_checks(True) is False
+    with maxsim_amd.host_checks(False):
+        assert maxsim_amd._HOST_CHECKS is False
+        with maxsim_amd.host_checks(True):
+            assert maxsim_amd._HOST_CHECKS is True
+        assert maxsim_amd._HOST_CHECKS is False
+    assert maxsim_amd._HOST_CHECKS is True
+    import maxsim
+    assert maxsim.set_host_checks is maxsim_amd.set_host_checks
