@@ -158,6 +158,29 @@ def time_wall(torch, fn, reps, warmup):
 
 
 def cpu_model() -> str:
+    """The host CPU as ``lscpu`` names it (model name, vendor, family/model/
+    stepping, logical CPUs, hypervisor), else /proc/cpuinfo's model name."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        info = {}
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+        if info.get("Model name"):
+            parts = [info["Model name"]]
+            if info.get("Vendor ID"):
+                parts.append(info["Vendor ID"])
+            fms = "/".join(info.get(k, "?") for k in ("CPU family", "Model", "Stepping"))
+            parts.append(f"family/model/stepping {fms}")
+            if info.get("CPU(s)"):
+                parts.append(f"{info['CPU(s)']} logical CPUs")
+            if info.get("Hypervisor vendor"):
+                parts.append(f"hypervisor {info['Hypervisor vendor']}")
+            return ", ".join(parts)
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -165,6 +188,30 @@ def cpu_model() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def make_c1(torch, dev, seed=0, nq=8, C=16, lq=32, ld=300, dim=128):
+    """C1: padded rerank, fp32, Nq=8 x C=16, Lq=32, Ld padded to 300 with
+    lengths U[64, 300], L2-normalised Gaussian rows."""
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(nq, lq, dim, generator=g), dim=-1)
+    d = F.normalize(torch.randn(nq, C, ld, dim, generator=g), dim=-1)
+    dlen = torch.randint(64, ld + 1, (nq, C), generator=g, dtype=torch.int32)
+    qlen = torch.full((nq,), lq, dtype=torch.int32)
+    return q.to(dev), d.to(dev), qlen.to(dev), dlen.to(dev)
+
+
+def cpu_median(fn, reps, warmup):
+    """Median wall seconds of ``reps`` calls after ``warmup`` calls."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
 
 
 def profile_ops(torch, dev):
@@ -201,6 +248,78 @@ MATRIX_PADDED = [("Rerank", dict(B=32, C=50, Lq=32, Ld=180, dim=128)),
                  ("HeavyRerank", dict(B=32, C=100, Lq=32, Ld=256, dim=128))]
 MATRIX_PACKED = [("PackedRerank", dict(B=32, C=50, Lq=32, Ld=180, dim=128)),
                  ("PackedHeavyRerank", dict(B=32, C=100, Lq=32, Ld=256, dim=128))]
+
+
+def git_state() -> dict:
+    """The commit this tree was built from: git where the metadata is
+    present, else the record the native build wrote next to the libraries
+    (maxsim_amd/_build_info.json), else unknown."""
+    import subprocess
+
+    try:
+        head = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "HEAD"], capture_output=True,
+                              text=True, timeout=20)
+        if head.returncode == 0:
+            st = subprocess.run(["git", "-C", str(ROOT), "status", "--porcelain", "--",
+                                 "maxsim_amd", "include", "oracle", "bench.py"],
+                                capture_output=True, text=True, timeout=20)
+            return {"git_commit": head.stdout.strip(),
+                    "git_dirty": st.returncode == 0 and bool(st.stdout.strip())}
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        info = json.loads((ROOT / "maxsim_amd" / "_build_info.json").read_text())
+        return {"git_commit": str(info.get("git_commit", "unknown")),
+                "git_dirty": bool(info.get("git_dirty", False))}
+    except (OSError, ValueError):
+        return {"git_commit": "unknown", "git_dirty": False}
+
+
+def matrix_payload(runs, *, machine, n_iter, n_warm, repeats, started, wall) -> dict:
+    """The reference's v2 result record (scripts/bench_matrix.py:767-792)
+    from ``runs`` (one list of per-preset measurements per repeat): medians
+    over the repeats, backward time = step - forward, speedups and their
+    spread across repeats."""
+    def med(xs):
+        xs = [x for x in xs if x is not None]
+        return statistics.median(xs) if xs else None
+
+    def ratio(a, b):
+        return a / b if a is not None and b not in (None, 0) else None
+
+    results = []
+    for w in range(len(runs[0])):
+        per = [r[w] for r in runs]
+        base = per[0]
+        k, n = med([r["k"] for r in per]), med([r["n"] for r in per])
+        kf, nf = med([r["kf"] for r in per]), med([r["nf"] for r in per])
+        kb = max(k - kf, 0.0) if kf is not None else None
+        nb = max(n - nf, 0.0) if nf is not None else None
+        kmb, nmb = med([r["kmb"] for r in per]), med([r["nmb"] for r in per])
+        speedups = [r["n"] / r["k"] for r in per]
+        variance = ({"step_speedup_min": min(speedups), "step_speedup_max": max(speedups),
+                     "step_speedup_spread": max(speedups) - min(speedups),
+                     "step_speedup_stdev": statistics.stdev(speedups), "n_repeats": len(per)}
+                    if len(per) >= 2 else {"n_repeats": len(per)})
+        results.append({
+            "surface": base["surface"], "preset": base["preset"], "description": "",
+            "shape": base["shape"], "dtype": base["dtype"],
+            "maxsim_step_ms": k, "naive_step_ms": n, "step_speedup": ratio(n, k),
+            "maxsim_fwd_ms": kf, "naive_fwd_ms": nf,
+            "padded_ms": med([r["padded"] for r in per]),
+            "maxsim_bwd_ms": kb, "naive_bwd_ms": nb, "bwd_speedup": ratio(nb, kb),
+            "maxsim_peak_mb": kmb, "naive_peak_mb": nmb, "peak_ratio": ratio(nmb, kmb),
+            "retained_reduction": base["red"], "correct": all(r["correct"] for r in per),
+            "note": "", "variance": variance,
+        })
+    return {
+        "schema_version": 1,
+        "kernel": {"repo": "maxsim-mi355x", "version": 2, **git_state()},
+        "machine": machine,
+        "bench": {"iters_per_repeat": n_iter, "warmup": n_warm, "repeats": repeats,
+                  "started_at": started, "wall_seconds": round(wall, 1)},
+        "results": results,
+    }
 
 
 def run_matrix(args, torch, dev):
@@ -355,53 +474,15 @@ def run_matrix(args, torch, dev):
     t0 = time.perf_counter()
     runs = [one_matrix() for _ in range(args.matrix_repeats)]
     wall = time.perf_counter() - t0
-
-    def med(vals):
-        vals = [v for v in vals if v is not None]
-        return statistics.median(vals) if vals else None
-
-    def ratio(a, b):
-        return a / b if a is not None and b not in (None, 0) else None
-
-    results = []
-    for w in range(len(runs[0])):
-        per = [r[w] for r in runs]
-        base = per[0]
-        k, n = med([r["k"] for r in per]), med([r["n"] for r in per])
-        kf, nf = med([r["kf"] for r in per]), med([r["nf"] for r in per])
-        kb = max(k - kf, 0.0) if kf is not None else None
-        nb = max(n - nf, 0.0) if nf is not None else None
-        kmb, nmb = med([r["kmb"] for r in per]), med([r["nmb"] for r in per])
-        speedups = [r["n"] / r["k"] for r in per]
-        variance = ({"step_speedup_min": min(speedups), "step_speedup_max": max(speedups),
-                     "step_speedup_spread": max(speedups) - min(speedups),
-                     "step_speedup_stdev": statistics.stdev(speedups), "n_repeats": len(per)}
-                    if len(per) >= 2 else {"n_repeats": len(per)})
-        results.append({
-            "surface": base["surface"], "preset": base["preset"], "description": "",
-            "shape": base["shape"], "dtype": base["dtype"],
-            "maxsim_step_ms": k, "naive_step_ms": n, "step_speedup": ratio(n, k),
-            "maxsim_fwd_ms": kf, "naive_fwd_ms": nf,
-            "padded_ms": med([r["padded"] for r in per]),
-            "maxsim_bwd_ms": kb, "naive_bwd_ms": nb, "bwd_speedup": ratio(nb, kb),
-            "maxsim_peak_mb": kmb, "naive_peak_mb": nmb, "peak_ratio": ratio(nmb, kmb),
-            "retained_reduction": base["red"], "correct": all(r["correct"] for r in per),
-            "note": "", "variance": variance,
-        })
     props = torch.cuda.get_device_properties(dev)
-    payload = {
-        "schema_version": 1,
-        "kernel": {"repo": "maxsim-mi355x", "version": 2, "git_commit": "unknown",
-                   "git_dirty": False},
-        "machine": {"gpu_name": torch.cuda.get_device_name(dev),
-                    "compute_capability": getattr(props, "gcnArchName", "gfx950"),
-                    "torch_version": torch.__version__,
-                    "cuda_version": getattr(torch.version, "hip", None)},
-        "bench": {"iters_per_repeat": n_iter, "warmup": n_warm, "repeats": args.matrix_repeats,
-                  "started_at": started.strftime("%Y-%m-%dT%H:%M:%SZ"),
-                  "wall_seconds": round(wall, 1)},
-        "results": results,
-    }
+    machine = {"gpu_name": torch.cuda.get_device_name(dev),
+               "compute_capability": getattr(props, "gcnArchName", "gfx950"),
+               "torch_version": torch.__version__,
+               "cuda_version": getattr(torch.version, "hip", None)}
+    payload = matrix_payload(runs, machine=machine, n_iter=n_iter, n_warm=n_warm,
+                             repeats=args.matrix_repeats,
+                             started=started.strftime("%Y-%m-%dT%H:%M:%SZ"), wall=wall)
+    results = payload["results"]
     with open(args.matrix, "w") as f:
         f.write(json.dumps(payload, indent=2) + "\n")
     log(f"matrix: wrote {args.matrix}")
@@ -507,9 +588,21 @@ def main():
     log(f"C5: step {ms_step:.3f} ms, fwd {ms_fwd:.3f} ms ({fwd_tflops:.1f} TFLOP/s), bwd {ms_bwd:.3f} ms")
 
     if not args.quick:
+        # ---------------- C1: small padded rerank, fp32 ----------------
+        log("C1: padded rerank 8x16, fp32")
+        q1, d1, ql1, dl1 = make_c1(torch, dev)
+        B1, C1_, Lq1, Ld1 = d1.shape[0], d1.shape[1], q1.shape[1], d1.shape[2]
+        qf1, df1 = q1.reshape(B1 * Lq1, -1), d1.reshape(B1 * C1_ * Ld1, -1)
+        dlf1 = dl1.reshape(-1)
+        ms1k = time_events(torch, lambda: ops.maxsim_padded_forward_with_argmax(
+            qf1, ql1, df1, dlf1, Lq1, Ld1, C1_), K, 2)
+        ms1a = time_wall(torch, lambda: maxsim_amd.score_candidates_padded_with_argmax(
+            q1, d1, ql1, dl1), K, 2)
+        extra["c1"] = {"kernel_ms": round(ms1k, 4), "api_call_ms": round(ms1a, 4)}
+
         # ---------------- C2: small contrastive step ----------------
         log("C2: contrastive 64x64")
-        q2, d2, off2, _ = make_c5(torch, dev, seed=1, nq=64, nb=64, lo=64, hi=512, dup=0.0)
+        q2, d2, off2, lens2 = make_c5(torch, dev, seed=1, nq=64, nb=64, lo=64, hi=512, dup=0.0)
         q2g, d2g = q2.clone().requires_grad_(True), d2.clone().requires_grad_(True)
         t2 = torch.arange(64, device=dev)
 
@@ -628,7 +721,11 @@ def main():
         extra["c4"] = {"fwd_ms": round(ms4f, 4), "bwd_ms": round(ms4b, 4),
                        "api_train_step_ms": round(api4, 4)}
 
-    # ---------------- CPU baseline (bounded sample of C5) ----------------
+    # ---------------- CPU baseline ----------------
+    # The reference's naive PyTorch formulation (einsum + max, fp32; autograd
+    # for the backward) on the host's cores: C5 on a bounded sample of query
+    # rows (the headline's cpu_baseline), C1 and C2 in full, C3 on a fixed
+    # subset of queries, C4 on a fixed subset of pairs.
     cpu = None
     if not args.no_cpu:
         from oracle import torch_baseline
@@ -636,26 +733,54 @@ def main():
         # the GPU box's CPU share is 16 threads whatever the affinity mask shows
         cores = min(16, len(os.sched_getaffinity(0)))
         torch.set_num_threads(cores)
+        host = cpu_model()
         nsample = 64
         qc = q[:nsample].float().cpu()
         dc, mask = torch_baseline.pad_documents(d.float().cpu(), lens)
         rows = torch.arange(nsample)
-        log(f"CPU baseline: {nsample} of {nq} query rows x {nb} docs on {cores} threads")
-        for _ in range(2):  # warmup
-            torch_baseline.contrastive_step(qc, rows, dc, mask, nq)
-        times = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            torch_baseline.contrastive_step(qc, rows, dc, mask, nq)
-            times.append(time.perf_counter() - t0)
-        t_sample = statistics.median(times)
+        log(f"CPU baseline: {nsample} of {nq} query rows x {nb} docs on {cores} threads ({host})")
+        t_sample = cpu_median(lambda: torch_baseline.contrastive_step(qc, rows, dc, mask, nq), 5, 2)
         cpu_tflops = (flops_fwd * nsample / nq) / t_sample / 1e12
         cpu = {"value": round(cpu_tflops, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
                "sample": f"C5 fwd+CE+bwd for {nsample}/{nq} query rows against all {nb} docs "
                          f"(fp32 einsum+max, -inf masked padding to Ld_max), median of 5 after 2 warmups; "
-                         f"{t_sample:.3f} s per sample step; host CPU: {cpu_model()}",
-               "step_ms_extrapolated": round(t_sample * nq / nsample * 1e3, 1)}
+                         f"{t_sample:.3f} s per sample step; host CPU: {host}",
+               "step_ms_extrapolated": round(t_sample * nq / nsample * 1e3, 1),
+               "host": host}
         log(f"CPU baseline: {t_sample:.3f} s per sample -> {cpu_tflops:.4f} TFLOP/s")
+        if not args.quick:
+            legs = {}
+            # C1 in full: padded scores + argmax, fp32
+            c1c = [t.cpu() for t in (q1, d1, ql1, dl1)]
+            t1 = cpu_median(lambda: torch_baseline.padded_scores_with_argmax(*c1c), 5, 2)
+            legs["c1"] = {"ms": round(t1 * 1e3, 3), "what": "padded fwd + argmax, 8x16, in full"}
+            # C2 in full: fwd + CE(diagonal) + bwd
+            dc2, mask2 = torch_baseline.pad_documents(d2.float().cpu(), lens2)
+            q2c = q2.float().cpu()
+            t2 = cpu_median(lambda: torch_baseline.contrastive_step(q2c, torch.arange(64), dc2,
+                                                                    mask2, 64), 5, 2)
+            legs["c2"] = {"step_ms": round(t2 * 1e3, 2), "what": "fwd+CE+bwd, 64x64, in full"}
+            # C3 on queries 0, 97, 255 (chunk-seeded: bit-identical to those rows of the full set)
+            sub = [0, 97, 255]
+            q3s, d3s, ql3s, dl3s = make_c3(torch, dev, only=sub)
+            c3c = (q3s.float().cpu(), d3s.float().cpu(), ql3s.cpu(), dl3s.cpu())
+            del q3s, d3s
+            t3 = cpu_median(lambda: torch_baseline.padded_scores(*c3c), 3, 1)
+            legs["c3"] = {"docs_per_s": round(len(sub) * c3c[1].shape[1] / t3, 1),
+                          "what": f"padded fwd, queries {sub} x 1000 candidates (fp16 inputs in fp32)"}
+            # C4 on its first 2,000 pairs (the pair ids are uniform random):
+            # fwd + bwd with the upstream gradient; the full step is ~10x
+            n4 = 2000
+            c4c = [t.cpu() for t in (q4, qo4, d4, do4, qi4[:n4], di4[:n4])]
+            c4c[0], c4c[2] = c4c[0].float(), c4c[2].float()
+            g4c = g4[:n4].cpu()
+            t4 = cpu_median(lambda: torch_baseline.packed_step(*c4c, g4c), 3, 1)
+            legs["c4"] = {"sample_step_ms": round(t4 * 1e3, 1),
+                          "step_ms_extrapolated": round(t4 * 1e3 * qi4.numel() / n4, 1),
+                          "what": f"packed fwd+bwd on the first {n4} of {qi4.numel()} pairs "
+                                  "(pairs by document length, padded chunks)"}
+            cpu["legs"] = legs
+            log("CPU legs: " + ", ".join(f"{k} {v}" for k, v in legs.items()))
 
     value = flops_fwd / (ms_step * 1e-3) / 1e12
     out = {

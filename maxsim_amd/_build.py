@@ -106,9 +106,35 @@ def build_torch_binding() -> Path:
     return TORCH_LIB
 
 
+BUILD_INFO = PKG / "_build_info.json"
+
+
+def write_build_info() -> None:
+    """Record the source revision the libraries were built from
+    (``_build_info.json``, next to them): the GPU box receives the tree
+    without its git metadata, and the benchmark's result records name the
+    commit."""
+    import json
+
+    info = {"git_commit": "unknown", "git_dirty": False}
+    try:
+        head = subprocess.run(["git", "-C", str(REPO), "rev-parse", "HEAD"],
+                              capture_output=True, text=True, timeout=20)
+        if head.returncode == 0:
+            info["git_commit"] = head.stdout.strip()
+            st = subprocess.run(["git", "-C", str(REPO), "status", "--porcelain", "--",
+                                 "maxsim_amd", "include", "oracle", "bench.py"],
+                                capture_output=True, text=True, timeout=20)
+            info["git_dirty"] = st.returncode == 0 and bool(st.stdout.strip())
+    except (OSError, subprocess.SubprocessError):
+        pass
+    BUILD_INFO.write_text(json.dumps(info) + "\n")
+
+
 def build() -> None:
     build_hip_library()
     build_torch_binding()
+    write_build_info()
 
 
 if __name__ == "__main__":

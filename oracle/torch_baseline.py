@@ -59,3 +59,52 @@ def padded_scores(q: torch.Tensor, d: torch.Tensor, qlen: torch.Tensor, dlen: to
     best = sim.max(dim=-1).values
     qmask = torch.arange(Lq)[None, :] < qlen[:, None]
     return best.masked_fill(~qmask[:, None, :], 0.0).sum(dim=-1)
+
+
+def padded_scores_with_argmax(q: torch.Tensor, d: torch.Tensor, qlen: torch.Tensor,
+                              dlen: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """As :func:`padded_scores`, plus the argmax ``[B, C, Lq]`` (0 beyond a
+    query's length)."""
+    Lq, Ld = q.shape[1], d.shape[2]
+    sim = torch.einsum("bid,bcjd->bcij", q, d)
+    dmask = torch.arange(Ld)[None, None, :] < dlen[:, :, None]
+    sim = sim.masked_fill(~dmask[:, :, None, :], float("-inf"))
+    best, idx = sim.max(dim=-1)
+    qmask = torch.arange(Lq)[None, :] < qlen[:, None]
+    return (best.masked_fill(~qmask[:, None, :], 0.0).sum(dim=-1),
+            idx.masked_fill(~qmask[:, None, :], 0).to(torch.int32))
+
+
+def packed_step(q: torch.Tensor, qoff: torch.Tensor, d: torch.Tensor, doff: torch.Tensor,
+                qids: torch.Tensor, dids: torch.Tensor, dscore: torch.Tensor,
+                budget: int = 1 << 25) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packed pairs forward + backward with upstream ``dscore [P]``: pairs in
+    order of document length, gathered into padded chunks of at most
+    ``budget`` similarity entries (-inf past a document, 0 past a query),
+    einsum + max + sum, autograd accumulating dQ and dD over the chunks.
+    Returns ``(dq, dd)``."""
+    qg = q.detach().clone().requires_grad_(True)
+    dg = d.detach().clone().requires_grad_(True)
+    ql = (qoff[1:] - qoff[:-1]).long()
+    dl = (doff[1:] - doff[:-1]).long()
+    qids, dids = qids.long(), dids.long()
+    order = torch.argsort(dl[dids], stable=True)
+    lq_max = int(ql.max())
+    P, c = order.numel(), 0
+    while c < P:
+        # the chunk grows while n * Lq_max * Ld (Ld of its last, longest pair) fits the budget
+        ld_last = int(dl[dids[order[min(P - 1, c)]]])
+        n = max(1, min(P - c, budget // max(1, lq_max * ld_last)))
+        idx = order[c:c + n]
+        qi, di = qids[idx], dids[idx]
+        Lq, Ld = int(ql[qi].max()), int(dl[di].max())
+        qmask = torch.arange(Lq)[None, :] < ql[qi][:, None]
+        dmask = torch.arange(Ld)[None, :] < dl[di][:, None]
+        qrow = torch.where(qmask, qoff[qi].long()[:, None] + torch.arange(Lq)[None, :], 0)
+        drow = torch.where(dmask, doff[di].long()[:, None] + torch.arange(Ld)[None, :], 0)
+        sim = torch.einsum("nid,njd->nij", qg[qrow], dg[drow])
+        sim = sim.masked_fill(~dmask[:, None, :], float("-inf"))
+        s = sim.max(dim=-1).values.masked_fill(~qmask, 0.0).sum(dim=-1)
+        (s * dscore[idx]).sum().backward()
+        c += n
+    return qg.grad, dg.grad

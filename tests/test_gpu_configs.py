@@ -74,6 +74,33 @@ def test_c3_padded_rerank_query_slice():
                  lambda idx, j: dn[idx[0], idx[1], j])
 
 
+def test_c3_full_size_rows_equal_the_checked_slice():
+    """C3 at full size (256 x 1000 x 300 x 128 fp16, 9.8e9 elements, well
+    past 2^31): rows 0, 97 and 255 of the scores and argmax equal, bit for
+    bit, those of the 3-query slice that the test above checks against the
+    oracle (each (query, candidate) is computed independently of the batch,
+    and the chunk-seeded inputs are identical), so addressing beyond 2^31
+    elements is pinned."""
+    only = [0, 97, 255]
+    qs, ds, qls, dls = bench.make_c3(torch, DEVICE, only=only)
+    s_slice, a_slice = maxsim_amd.score_candidates_padded_with_argmax(qs, ds, qls, dls)
+    del qs, ds
+    q, d, qlen, dlen = bench.make_c3(torch, DEVICE)
+    assert d.numel() > 2**33
+    try:
+        scores = maxsim_amd.score_candidates_padded(q, d, qlen, dlen)
+        s_full, a_full = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+        torch.cuda.synchronize()
+        assert torch.equal(scores, s_full)
+        assert torch.isfinite(s_full).all()
+        rows = torch.tensor(only, device=DEVICE)
+        assert torch.equal(s_full[rows], s_slice)
+        assert torch.equal(a_full[rows], a_slice)
+    finally:
+        del q, d
+        torch.cuda.empty_cache()
+
+
 def test_c4_packed_forward_and_backward_full():
     (q, qo, d, do, qi, di, mql, g, *_r) = bench.make_c4(torch, DEVICE)
     scores, argmax = maxsim_amd.score_pairs_packed_with_argmax(q, qo, d, do, qi, di)
