@@ -36,10 +36,11 @@ PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
 # HBM-side bytes per launch of the forward kernel at C5, from the two
 # rocprofv3 counter passes in profiles/c5_ops_hbm_traffic.md (FETCH_SIZE and
-# WRITE_SIZE per dispatch, each scaled by the reading for a 1 GiB copy:
-# x3.813 and x1.952).  Counters cannot be read from inside this process, so
-# the figure is the committed measurement, not a live one.
-FWD_TRAFFIC_BYTES_C5 = int((52934.4 * 3.813 + 33888.3 * 1.952) * 1024)
+# WRITE_SIZE per dispatch, each scaled by what the counter reads for this
+# build's own pack_rows_kernel copying 1 GiB: FETCH x1.997, WRITE x1.000).
+# Counters cannot be read from inside this process, so the figure is the
+# committed measurement, not a live one.
+FWD_TRAFFIC_BYTES_C5 = int((52934.7 * 1.997 + 33888.9 * 1.000) * 1024)
 
 
 def parse_args():
@@ -50,8 +51,9 @@ def parse_args():
     p.add_argument("--quick", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--profile-ops", action="store_true",
-                   help="run only the C5 operators (3x forward+argmax, 3x backward) and a "
-                        "1 GiB device copy, for rocprofv3 counter passes")
+                   help="run only the C5 operators (3x forward+argmax, 3x backward, 3x typed "
+                        "backward) and two calibration kernels of known bytes, for rocprofv3 "
+                        "counter passes")
     p.add_argument("--matrix", metavar="OUT_JSON",
                    help="run the reference's preset matrix (scripts/bench_matrix.py) instead and "
                         "write its v2 result schema to OUT_JSON")
@@ -215,8 +217,16 @@ def cpu_median(fn, reps, warmup):
 
 
 def profile_ops(torch, dev):
-    """C5 operators in isolation plus a plain copy of known size: the copy's
-    FETCH_SIZE / WRITE_SIZE readings calibrate the counters to bytes."""
+    """The C5 operators in isolation (3x forward with argmax, 3x the fp32
+    backward operator, 3x the typed backward of the training step), then two
+    of this build's own kernels whose HBM bytes are known exactly, to
+    calibrate the FETCH_SIZE / WRITE_SIZE counters to bytes:
+
+    * ``pack_rows_kernel`` copying 1 GiB of bf16 rows (every row valid):
+      reads 1 GiB and writes 1 GiB, each byte once, 16-byte accesses;
+    * ``pair_kernel`` (padded forward) over 1 GiB of fp16 candidate rows, all
+      lengths full: reads the candidates once (plus 0.25 MiB of queries) and
+      writes only the scores."""
     from maxsim_amd._ops import ops
 
     q, d, off, _ = make_c5(torch, dev)
@@ -226,12 +236,30 @@ def profile_ops(torch, dev):
     dscore = (torch.softmax(scores, dim=1) - torch.eye(nq, device=dev)) / nq
     for _ in range(3):
         ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
-    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
-    dst = torch.empty_like(src)
     for _ in range(3):
-        dst.copy_(src)
+        ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+    del q, d, scores, argmax
+    # calibration 1: a 1 GiB row copy through pack_rows_kernel
+    seg, ld, dim = 4096, 1024, 128
+    padded = torch.randn(seg * ld, dim, device=dev).to(torch.bfloat16)
+    lens = torch.full((seg,), ld, dtype=torch.int32, device=dev)
+    offs = torch.arange(0, (seg + 1) * ld, ld, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ops.maxsim_pack_padded_rows(padded, lens, offs, ld, seg * ld)
+    copy_bytes = padded.numel() * 2
+    del padded
+    # calibration 2: the padded forward reading 1 GiB of candidates once
+    B, C, Lq, Ld = 64, 256, 32, 256
+    qp = torch.randn(B * Lq, dim, device=dev).half()
+    dp = torch.randn(B * C * Ld, dim, device=dev).half()
+    ql = torch.full((B,), Lq, dtype=torch.int32, device=dev)
+    dl = torch.full((B * C,), Ld, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ops.maxsim_padded_forward(qp, ql, dp, dl, Lq, Ld, C)
     torch.cuda.synchronize()
-    print(json.dumps({"profile_ops": "c5", "copy_bytes": src.numel() * 4}), flush=True)
+    print(json.dumps({"profile_ops": "c5", "pack_copy_bytes": copy_bytes,
+                      "padded_read_bytes": dp.numel() * 2 + qp.numel() * 2,
+                      "padded_write_bytes": B * C * 4}), flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -803,6 +831,11 @@ def main():
                      "achieved": round(fwd_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": FWD_TRAFFIC_BYTES_C5,
+                     # algorithmic bytes of one forward launch: Q and D read,
+                     # scores and argmax written, each once
+                     "traffic_over_algorithmic": round(
+                         FWD_TRAFFIC_BYTES_C5 / (2 * dim * (nq * lq + total) + 4 * nq * nb
+                                                 + 4 * nq * nb * lq), 3),
                      "traffic_source": "profiles/c5_ops_hbm_traffic.md"},
         "cpu_baseline": cpu,
         "extra": extra,
