@@ -545,19 +545,21 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // instruction fills 1 KB of a buffer; the swizzle is applied by choosing
   // the source address of each slot).  Step k:
   //   (0) issue the first MFMAs of tile k+1 (operands already in registers);
-  //   (1) wait until this wave's loads of tile k+2 have landed, barrier --
-  //       now every wave's loads of tile k+2 are in LDS and every wave has
-  //       finished reading tile k's buffer (read two steps earlier);
-  //   (2) issue the loads of tile k+4 into tile k's buffer;
-  //   (3) issue the rest of tile k+1's MFMAs into one accumulator set, and
+  //   (1) on even k only: wait until this wave's loads of tiles k+2 and k+3
+  //       have landed, barrier -- now every wave's loads of both tiles are
+  //       in LDS and every wave has finished reading the buffers of tiles k
+  //       and k+1 (read two steps earlier, in steps k-2 and k-1) -- and
+  //       issue the loads of tiles k+4 and k+5 into those two buffers;
+  //   (2) issue the rest of tile k+1's MFMAs into one accumulator set, and
   //       read tile k+2's fragments;
-  //   (4) run the max/argmax epilogue of tile k from the other set -- its
+  //   (3) run the max/argmax epilogue of tile k from the other set -- its
   //       VALU work and the LDS reads are interleaved with the MFMAs;
-  //   (5) advance the load and epilogue cursors.
-  // Loads have two steps to land, operand reads a whole step, and no
-  // registers are spent on global->LDS staging.  Vector-memory loads
-  // complete in issue order, so "at most N loads outstanding"
-  // (s_waitcnt vmcnt(N)) identifies completed tiles.
+  //   (4) advance the load and epilogue cursors.
+  // Loads have two steps to land and operand reads a whole step; no
+  // registers are spent on global->LDS staging.  One barrier every two steps
+  // (rather than every step) halves the time waves spend waiting for the
+  // slowest one; the MFMAs issued before it keep the matrix pipe busy
+  // meanwhile.  Vector-memory loads complete in issue order.
   int ntiles = 0;
   for (int bl = 0; bl < n_docs; ++bl) {
     int s0;
@@ -651,8 +653,9 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // into block p % NBW, chunk p / NBW), so consecutive MFMAs are independent.
   // The first kPreMfma are issued before the step's wait and barrier (they
   // only read registers): the matrix pipe then has work while the waves
-  // synchronise and issue the scalar work that follows the barrier.
-  constexpr int kPreMfma = NBW;
+  // synchronise and issue the scalar work that follows the barrier.  Three
+  // of each block's chunks measured best (one or two: 1-2 % slower).
+  constexpr int kPreMfma = (3 * NBW < NBW * KS) ? 3 * NBW : NBW * KS;
   auto mfma_range = [&](auto lo_c, auto hi_c, const Frag<T> (&df)[KS],
                         f32x16 (&acc)[NBW]) __attribute__((always_inline)) {
 #pragma unroll
@@ -756,11 +759,14 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
     Frag<T> (&fr_nxt)[KS] = (U % 2 == 0) ? fr1 : fr0;   // tile k+1
     Frag<T> (&fr_new)[KS] = (U % 2 == 0) ? fr0 : fr1;   // <- tile k+2
     mfma_pre(fr_nxt, acc_nxt);
-    // tile k+2 must be resident; this wave's loads of k+2 and k+3 may still be
-    // outstanding (k+3 only if it exists)
-    wait_vm(k + 3 < ntiles ? d_w : 0);
-    barrier();
-    dma_tile(u_const, fc);                               // tile k+4 -> buffer k % 4
+    if constexpr (U % 2 == 0) {
+      // tiles k+2 and k+3 resident (every load of this wave landed), then
+      // tiles k+4 and k+5 -> the buffers of tiles k and k+1
+      wait_vm(0);
+      barrier();
+      dma_tile(u_const, fc);
+      dma_tile(std::integral_constant<int, U + 1>{}, advance(fc));
+    }
     // Past the last tile these reads and MFMAs see stale buffers; their
     // results are never used, and every wave keeps the same barrier count.
     read_frags(std::integral_constant<int, (U + 2) % kNB>{}, fr_new);
