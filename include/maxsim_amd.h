@@ -260,8 +260,8 @@ int maxsim_amd_contrastive_backward(
  * fp32 gradients and autograd casts them to the input dtype in a separate
  * pass; writing the input dtype directly removes that pass and halves the
  * document-gradient write.  A 16-bit grad_dtype needs the document gradient
- * in a single pass over the entries (num_queries * (Lq + 1) up to 18,430 on
- * gfx950); beyond that the call returns MAXSIM_ERR_UNSUPPORTED before
+ * in a single pass over the entries (num_queries * (Lq + 1) up to 38,910 on
+ * gfx950, whose workgroups may use 160 KB of LDS); beyond that the call returns MAXSIM_ERR_UNSUPPORTED before
  * launching anything, and the caller uses the fp32 form. */
 int maxsim_amd_contrastive_backward_typed(
     maxsim_dtype dtype, maxsim_dtype grad_dtype, const float* dscore,

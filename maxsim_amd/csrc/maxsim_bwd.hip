@@ -2574,11 +2574,22 @@ static int contrastive_backward_impl(
   da.part_slices = (nslices + da.parts - 1) / da.parts;
   da.group = 1;
   while (da.group < kDdMaxGroup && da.group < da.part_slices) da.group *= 2;
-  const size_t lds_cap = std::min<size_t>(max_lds_per_block(), 80 * 1024);
   da.rows_per_pass = 1024;
   const size_t bucket_bytes = 2 * (size_t)(da.rows_per_pass + 1) * sizeof(int);
-  int64_t e_cap = (int64_t)((lds_cap - bucket_bytes) / sizeof(int));
-  if (e_cap > 65535) e_cap = 65535;  // packed bucket ids hold x < 2^16
+  auto entry_cap = [&](size_t cap) {
+    const int64_t e = (int64_t)((cap - bucket_bytes) / sizeof(int));
+    return std::min<int64_t>(e, 65535);  // packed bucket ids hold x < 2^16
+  };
+  size_t lds_cap = std::min<size_t>(max_lds_per_block(), 80 * 1024);
+  int64_t e_cap = entry_cap(lds_cap);
+  // 16-bit output needs every entry in one pass (below): when 80 KB holds
+  // too few, take all the LDS a workgroup may have (one workgroup per CU)
+  // rather than the fp32 kernels plus a cast.
+  if (out16 && (Lq > e_cap || num_queries * (Lq + 1) > e_cap) &&
+      max_lds_per_block() > lds_cap) {
+    lds_cap = max_lds_per_block();
+    e_cap = entry_cap(lds_cap);
+  }
   // whole queries per pass when Lq fits (E ids + E / Lq staged dscore values),
   // else one query's tokens in chunks of E (one staged value)
   int64_t qpp = 1;

@@ -187,7 +187,8 @@ TYPED = [
     pytest.param(3, 16, 64, [37, 64, 200, 17, 81], id="Nb5-gather"),
     pytest.param(4, 32, 128, [40, 1, 300, 33, 90, 64, 7, 129, 2], id="Nb9-split"),
     pytest.param(2, 7, 20, [9, 33, 5, 1, 2, 70, 3, 8], id="dim20-element-wise"),
-    pytest.param(600, 32, 128, [64, 10, 200, 33, 1, 128, 90, 47, 300, 5], id="Nq600-fp32-fallback"),
+    pytest.param(600, 32, 128, [64, 10, 200, 33, 1, 128, 90, 47, 300, 5], id="Nq600-lds-pass"),
+    pytest.param(1200, 32, 64, [64, 10, 200, 33, 1, 28, 9], id="Nq1200-fp32-fallback"),
     pytest.param(1, 20000, 8, [3, 17, 1, 40, 9, 2, 5, 11], id="Lq20000-fp32-fallback"),
 ]
 
@@ -213,6 +214,40 @@ def test_contrastive_backward_typed_equals_cast_fp32(Nq, Lq, dim, d_lens, dtype)
     # absolute term sums of dd: the same routing with |dscore| and |q|
     _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
     assert_rounded_from(dd, dd32, mag)
+
+
+def test_contrastive_backward_typed_single_pass_limit():
+    """Through the C ABI: 16-bit gradients for Nq * (Lq + 1) = 19,800 entries
+    (beyond an 80 KB LDS pass, within the 160 KB a workgroup may use) are
+    written directly; 39,600 entries return MAXSIM_ERR_UNSUPPORTED before
+    any launch (the operator then takes the fp32 kernels and a cast)."""
+    import ctypes
+    from pathlib import Path
+
+    lib = ctypes.CDLL(str(Path(maxsim_amd.__file__).resolve().parent / "libmaxsim_amd.so"))
+    lib.maxsim_amd_last_error.restype = ctypes.c_char_p
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    fn = lib.maxsim_amd_contrastive_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P,
+                   ctypes.c_size_t, P]
+    BF16 = 2
+    for nq, ok in ((600, True), (1200, False)):
+        q, d, off = make_contrastive(nq, 32, 64, [64, 10, 200, 33], torch.bfloat16, seed=nq)
+        _, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+        dscore = torch.randn(nq, 4, generator=torch.Generator().manual_seed(1)).to(DEVICE)
+        dq = torch.empty_like(q)
+        dd = torch.empty_like(d)
+        rc = fn(BF16, BF16, dscore.data_ptr(), q.data_ptr(), nq, 32, d.data_ptr(), d.shape[0],
+                off.data_ptr(), 4, argmax.data_ptr(), 64, dq.data_ptr(), dd.data_ptr(), None, 0,
+                torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        if ok:
+            assert rc == 0, lib.maxsim_amd_last_error()
+            dq32, dd32 = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+            _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
+            assert_rounded_from(dd, dd32, mag)
+        else:
+            assert rc != 0 and b"16-bit" in lib.maxsim_amd_last_error()
 
 
 def test_contrastive_backward_typed_fp32_inputs_are_fp32():
