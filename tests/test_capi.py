@@ -155,9 +155,10 @@ def test_typed_backward_rejects_a_third_grad_dtype(lib):
 
 
 def test_typed_backward_16bit_needs_one_entry_pass(lib):
-    # 1000 x 32 entries exceed one LDS pass of the document gradient: refused
-    # before any launch, so the caller can take the fp32 path
-    assert _typed_backward(lib, nq=1000, lq=32) == UNSUPPORTED
+    # 1300 x 33 entries exceed one LDS pass of the document gradient (even
+    # with all 160 KB of a gfx950 workgroup): refused before any launch, so
+    # the caller can take the fp32 path
+    assert _typed_backward(lib, nq=1300, lq=32) == UNSUPPORTED
     assert b"fp32" in lib.maxsim_amd_last_error()
     # one query whose tokens alone exceed a pass (token chunks): refused too
     assert _typed_backward(lib, nq=1, lq=40000) == UNSUPPORTED
