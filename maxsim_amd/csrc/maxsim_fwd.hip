@@ -16,7 +16,9 @@
 //    (reference K1/K2/K3/K5/K9, maxsim.cu:70-322, 647-698, 1933-2010).  Used
 //    for padded rerank and packed pairs, whose document tiles are each used
 //    by a single query (HBM-bound), and for contrastive shapes the tiled
-//    kernel does not cover (Lq > 64).
+//    kernel does not cover (Lq > 64).  pair_ring_kernel is its variant for
+//    16-bit rows of at most 128 elements and queries of at most 64 tokens:
+//    tiles come in through two wave-private LDS slots, two tiles ahead.
 //
 // Neither kernel writes the [Lq, Ld] similarity matrix anywhere: each
 // 32x32 MFMA tile is reduced in registers (tile_update) and discarded.
@@ -792,6 +794,168 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
 }
 
 // ---------------------------------------------------------------------------
+// pair_ring_kernel: pair_kernel's work split (one wave per run of `ppw`
+// pairs, queries of at most two 32-token blocks in registers) with the
+// document tiles brought in by direct global->LDS loads into two
+// wave-private LDS slots, two tiles ahead, in place of pair_kernel's one tile
+// ahead in registers.  Packed pairs and padded candidates miss L2 on nearly
+// every tile and the MFMA pipe is mostly idle, so the time is the latency of
+// the tile loads: twice the tiles in flight per wave, at no register cost
+// (the staging registers are freed).  The load stream runs across pairs:
+// the next pair's first tiles load during the current pair's last ones.
+// No barriers: each wave owns its slots.  Same MFMA order and tile epilogue
+// as pair_kernel, so the results are bit-identical.
+// ---------------------------------------------------------------------------
+constexpr int kRingSlots = 2;
+constexpr int kRingWaves = 4;
+
+template <typename T, int KS, bool ARGMAX>
+__global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, int ppw) {
+  using S = typename T::storage;
+  using G = TileGeom<T, KS>;
+  static_assert(T::bytes == 2, "16-bit operands: one 16-byte piece per fragment");
+  constexpr int QB = 2;
+  constexpr int kRPI = 64 / G::P;          // tile rows per wave load instruction
+  constexpr int kDma = G::kPieces / 64;    // wave load instructions per tile
+  extern __shared__ uint4 lds[];
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t wave = (int64_t)blockIdx.x * kRingWaves + wv;
+  const int64_t p_begin = wave * ppw;
+  if (p_begin >= a.npairs) return;
+  const int64_t p_end = min(p_begin + (int64_t)ppw, a.npairs);
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(S);
+  const uint4* ring = lds + (size_t)wv * kRingSlots * G::kBufPieces;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+  // lane -> (row within an instruction's rows, piece); slot i*64 + lane of a
+  // tile holds piece (lo ^ (row & SWZ)) of row i*kRPI + hi
+  const int l_hi = lane / G::P;
+  const int l_lo = lane - l_hi * G::P;
+  int aoff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) aoff[s] = c * G::P + ((2 * s + h) ^ (c & G::SWZ));
+
+  // ---- load stream: the valid pairs' tiles in order
+  int64_t lp = p_begin;
+  Pair lpr = resolve_pair(a, lp);
+  while (!lpr.ok && ++lp < p_end) lpr = resolve_pair(a, lp);
+  int lt = 0;
+  int issued = 0;  // stream tiles whose loads were issued
+  auto dma_next = [&]() __attribute__((always_inline)) {
+    if (lp >= p_end) return;
+    const int slot = issued % kRingSlots;
+    const S* base = D + (lpr.d_row0 + (int64_t)lt * kTileRows) * dim;
+    const int last = lpr.ld - 1 - lt * kTileRows;
+#pragma unroll
+    for (int i = 0; i < kDma; ++i) {
+      const int r = i * kRPI + l_hi;
+      const uint32_t off = (uint32_t)min(r, last) * row_bytes +
+                           (uint32_t)((l_lo ^ (r & G::SWZ)) * 16);
+      lds_dma16(base, off, ring_lds + (uint32_t)((slot * G::kBufPieces + i * 64) * sizeof(uint4)));
+    }
+    ++issued;
+    if (++lt * kTileRows >= lpr.ld) {
+      lt = 0;
+      do {
+        ++lp;
+      } while (lp < p_end && !(lpr = resolve_pair(a, lp)).ok);
+    }
+  };
+  // s_waitcnt vmcnt(n), n = kDma (the next tile's loads may be outstanding) or 0
+  auto wait_tile = [&](bool next_issued) __attribute__((always_inline)) {
+    if (next_issued) {
+      if constexpr (kDma == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
+      else if constexpr (kDma == 4) __builtin_amdgcn_s_waitcnt(0x0F74);
+      else if constexpr (kDma == 2) __builtin_amdgcn_s_waitcnt(0x0F72);
+      else __builtin_amdgcn_s_waitcnt(0x0F70);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    __asm__ __volatile__("" ::: "memory");
+  };
+  dma_next();
+  dma_next();
+
+  Frag<T> qf[QB][KS];
+  int k = 0;  // stream index of the tile being computed
+  for (int64_t p = p_begin; p < p_end; ++p) {
+    const Pair pr = resolve_pair(a, p);
+    if (!pr.ok) {
+      write_invalid_pair(a, p, lane);
+      continue;
+    }
+    const int nblk = (pr.lq + kTileCols - 1) / kTileCols;  // <= QB (host checks)
+    const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (qb >= nblk) break;
+      const int tok = min(qb * kTileCols + c, pr.lq - 1);
+      const S* row = Q + (pr.q_row0 + tok) * (int64_t)dim;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[qb][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, true);
+    }
+    float m[QB];
+    int am[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      m[qb] = -__builtin_inff();
+      am[qb] = 0;
+    }
+    auto walk = [&](auto na_const) __attribute__((always_inline)) {
+      constexpr int NA = decltype(na_const)::value;
+      for (int t = 0; t < ntiles; ++t, ++k) {
+        wait_tile(issued > k + 1);
+        const uint4* tile = ring + (k % kRingSlots) * G::kBufPieces;
+        Frag<T> df[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) df[s].v = tile[aoff[s]];
+        f32x16 acc[NA];
+#pragma unroll
+        for (int qb = 0; qb < NA; ++qb) {
+          acc[qb] = f32x16{};
+#pragma unroll
+          for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
+        }
+        // the slot's fragments are in registers: refill it with the tile two
+        // ahead (lgkmcnt(0): the reads have completed)
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __asm__ __volatile__("" ::: "memory");
+        dma_next();
+#pragma unroll
+        for (int qb = 0; qb < NA; ++qb)
+          tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
+      }
+    };
+    if (nblk == 1)
+      walk(std::integral_constant<int, 1>{});
+    else
+      walk(std::integral_constant<int, QB>{});
+    float score = 0.0f;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (qb < nblk) {
+        merge_halves(m[qb], am[qb]);
+        const int tok = qb * kTileCols + c;
+        const bool valid = tok < pr.lq;
+        score += half_sum(valid ? m[qb] : 0.0f);
+        if (ARGMAX && h == 0 && tok < a.slots) a.argmax[p * a.slots + tok] = valid ? am[qb] : 0;
+      }
+    }
+    if (ARGMAX) {
+      for (int t = nblk * kTileCols + lane; t < a.slots; t += 64) a.argmax[p * a.slots + t] = 0;
+    }
+    if (lane == kHalfSumLane) a.scores[p] = score;
+  }
+  // drain: no load may still be writing LDS when the wave exits
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// ---------------------------------------------------------------------------
 // Host-side dispatch
 // ---------------------------------------------------------------------------
 static int ks_for_dim(int dim) {
@@ -865,6 +1029,25 @@ static void launch_wide(const FwdArgs& a, bool vec, hipStream_t st) {
     hipLaunchKernelGGL((wide_pair_kernel<T, false, false>), grid, dim3(256), 0, st, a);
 }
 
+template <typename T, int KS>
+static void launch_ring_ks(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
+  using G = TileGeom<T, KS>;
+  const size_t lds = (size_t)kRingWaves * kRingSlots * G::kBufPieces * sizeof(uint4);
+  if (a.argmax)
+    hipLaunchKernelGGL((pair_ring_kernel<T, KS, true>), grid, dim3(kRingWaves * 64), lds, st, a, ppw);
+  else
+    hipLaunchKernelGGL((pair_ring_kernel<T, KS, false>), grid, dim3(kRingWaves * 64), lds, st, a, ppw);
+}
+
+template <typename T>
+static void launch_ring(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
+  switch (ks_for_dim(a.dim)) {
+    case 2: launch_ring_ks<T, 2>(a, ppw, grid, st); break;
+    case 4: launch_ring_ks<T, 4>(a, ppw, grid, st); break;
+    default: launch_ring_ks<T, 8>(a, ppw, grid, st); break;
+  }
+}
+
 static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
                     hipStream_t st) {
   if (a.dim > kMaxRegDim) {
@@ -882,6 +1065,18 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
   const int ppw = pairs_per_wave(a.npairs);
   const bool vec = (a.dim == ks_for_dim(a.dim) * kChunk) && aligned16(a.q) &&
                    aligned16(a.d);
+  // 16-bit rows of at most 128 elements, queries of at most two blocks:
+  // the LDS-ring variant (two tiles in flight per wave)
+  if (dtype != MAXSIM_FLOAT32 && vec && ks_for_dim(a.dim) <= 8 && max_lq <= 2 * kTileCols &&
+      a.mode != kContrastive) {
+    const int64_t waves = (a.npairs + ppw - 1) / ppw;
+    const dim3 grid((unsigned)((waves + kRingWaves - 1) / kRingWaves));
+    switch (dtype) {
+      case MAXSIM_BFLOAT16: launch_ring<BF16>(a, ppw, grid, st); break;
+      default: launch_ring<F16>(a, ppw, grid, st); break;
+    }
+    return check_launch("pair_ring_kernel");
+  }
   switch (dtype) {
     case MAXSIM_BFLOAT16: launch_pair<BF16>(a, max_lq, ppw, vec, st); break;
     case MAXSIM_FLOAT16: launch_pair<F16>(a, max_lq, ppw, vec, st); break;
