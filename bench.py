@@ -615,6 +615,19 @@ def main():
     }
     log(f"C5: step {ms_step:.3f} ms, fwd {ms_fwd:.3f} ms ({fwd_tflops:.1f} TFLOP/s), bwd {ms_bwd:.3f} ms")
 
+    # One GPU's shard of C5 split by query rows over 8 GPUs (64 of the 512
+    # queries against all 512 documents): the kernels at the shape each rank
+    # would run, without the collectives (one GPU here).
+    qs = q[:64].contiguous()
+    ms_sf = time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(qs, d, off), K, 2)
+    s_s, a_s = ops.maxsim_contrastive_forward_with_argmax(qs, d, off)
+    g_s = dscore[:64].contiguous()
+    ms_sb = time_events(torch, lambda: ops.maxsim_contrastive_backward_typed(g_s, qs, d, off, a_s), K, 2)
+    extra["c5_shard_of_8"] = {"Nq": 64, "Nb": nb, "fwd_ms": round(ms_sf, 4),
+                              "fwd_tflops": round(flops_fwd / 8 / (ms_sf * 1e-3) / 1e12, 2),
+                              "bwd_typed_ms": round(ms_sb, 4)}
+    del s_s, a_s
+
     if not args.quick:
         # ---------------- C1: small padded rerank, fp32 ----------------
         log("C1: padded rerank 8x16, fp32")
