@@ -1024,14 +1024,19 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
 //     the (query, token) of an entry needs no division: a thread's entries
 //     are x = tid + 512 k, so when Lq divides 512 the token is fixed and the
 //     query advances by 512 / Lq;
-//   * a lane owns two slices (16 elements) of its group's row, so an
-//     entry's decode (row offset, weight) is shared by 16 elements;
 //   * Q rows are addressed as one 32-bit offset from a uniform base (one
-//     24-bit multiply-add per entry), and four entries (eight 16-byte
-//     loads) are in flight per lane.
+//     24-bit multiply-add per entry), and eight entries (eight 16-byte
+//     loads) are in flight per lane;
+//   * the groups of a wave run in lockstep, so a wave's time per round of
+//     rows is its largest bucket: rows are visited in decreasing bucket
+//     size (a counting sort of the rows by size class), so that the rows
+//     of a round have about the same size (documents of at least
+//     kBkOrderMin entries; below that the sort costs more than it saves).
 // ---------------------------------------------------------------------------
 constexpr int kBkBatch = 8;            // bucket entries gathered per step
 constexpr int kBkMaxEntriesPerThread = 32;
+constexpr int kBkClasses = 256;        // row size classes: ceil(entries / 4), capped
+constexpr int kBkOrderMin = 4096;      // entries per document from which rows are ordered
 
 template <typename T, int NS, typename O>
 __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
@@ -1153,8 +1158,51 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
       }
     }
     __syncthreads();
-    // 4. per-row fp32 sums: a group of G lanes per row, two slices per lane
-    for (int rr = grp; rr < nrows; rr += ngroups) {
+    // 4. row order: decreasing size class ceil(n / 4) (counting sort; the
+    // class table and the order use the cursor array, free after the
+    // scatter: kBkClasses ints, then nrows 16-bit row ids).  Small entry
+    // sets keep the natural order.
+    const bool ordered = ne >= kBkOrderMin;
+    int* chist = cursor;
+    uint16_t* order = reinterpret_cast<uint16_t*>(cursor + kBkClasses);
+    auto row_class = [&](int x) {
+      return kBkClasses - 1 - min((start[x + 1] - start[x] + 3) >> 2, kBkClasses - 1);
+    };
+    if (ordered) {
+      for (int x = tid; x < kBkClasses; x += kDdThreads) chist[x] = 0;
+      __syncthreads();
+      for (int x = tid; x < nrows; x += kDdThreads) atomicAdd(&chist[row_class(x)], 1);
+      __syncthreads();
+      if (tid < 64) {
+        constexpr int per = kBkClasses / 64;
+        int c[per];
+        int run = 0;
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+          c[k] = chist[lane * per + k];
+          run += c[k];
+        }
+        int incl = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int v = __shfl_up(incl, off);
+          if (lane >= off) incl += v;
+        }
+        int acc = incl - run;
+#pragma unroll
+        for (int k = 0; k < per; ++k) {
+          chist[lane * per + k] = acc;
+          acc += c[k];
+        }
+      }
+      __syncthreads();
+      for (int x = tid; x < nrows; x += kDdThreads)
+        order[atomicAdd(&chist[row_class(x)], 1)] = (uint16_t)x;
+      __syncthreads();
+    }
+    // 5. per-row fp32 sums: a group of G lanes per row, NS slices per lane
+    for (int ix = grp; ix < nrows; ix += ngroups) {
+      const int rr = ordered ? (int)order[ix] : ix;
       float acc[NS][8];
 #pragma unroll
       for (int u = 0; u < NS; ++u)
@@ -1169,21 +1217,23 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
         for (int u = 0; u < NS; ++u)
 #pragma unroll
           for (int e = 0; e < 8; ++e) blk[u][e] = 0.0f;
-        auto batch = [&](int s, auto masked) {
+        // KB entries from s (KB = 8, or 4 for a short tail)
+        auto batch = [&](int s, auto masked, auto kb) {
           constexpr bool MASKED = decltype(masked)::value;
-          uint32_t off[kBkBatch];
-          float gx[kBkBatch];
-          bool ok[kBkBatch];
+          constexpr int KB = decltype(kb)::value;
+          uint32_t off[KB];
+          float gx[KB];
+          bool ok[KB];
 #pragma unroll
-          for (int k = 0; k < kBkBatch; ++k) {
+          for (int k = 0; k < KB; ++k) {
             ok[k] = !MASKED || s + k < s1;
             const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
             off[k] = __umul24(v & 0xffffu, row_bytes) + k0b;
             gx[k] = gst[v >> 16];
           }
-          Frag<T> f[kBkBatch][NS];
+          Frag<T> f[KB][NS];
 #pragma unroll
-          for (int k = 0; k < kBkBatch; ++k)
+          for (int k = 0; k < KB; ++k)
 #pragma unroll
             for (int u = 0; u < NS; ++u) {
               const uint32_t o = off[k] + (uint32_t)u * 8u * (uint32_t)sizeof(S);
@@ -1200,7 +1250,7 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
           // each of its sums
           if constexpr (MASKED) {
 #pragma unroll
-            for (int k = 0; k < kBkBatch; ++k) {
+            for (int k = 0; k < KB; ++k) {
               if (!ok[k]) {
                 gx[k] = 0.0f;
 #pragma unroll
@@ -1209,16 +1259,21 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
             }
           }
 #pragma unroll
-          for (int k = 0; k < kBkBatch; ++k)
+          for (int k = 0; k < KB; ++k)
 #pragma unroll
             for (int u = 0; u < NS; ++u)
 #pragma unroll
               for (int e = 0; e < 8; ++e)
                 blk[u][e] = fmaf(gx[k], frag_elem(f[k][u], e), blk[u][e]);
         };
+        using B8 = std::integral_constant<int, kBkBatch>;
+        using B4 = std::integral_constant<int, kBkBatch / 2>;
         int s = s0;
-        for (; s + kBkBatch <= s1; s += kBkBatch) batch(s, std::false_type{});
-        if (s < s1) batch(s, std::true_type{});
+        for (; s + kBkBatch <= s1; s += kBkBatch) batch(s, std::false_type{}, B8{});
+        if (s1 - s > kBkBatch / 2)
+          batch(s, std::true_type{}, B8{});
+        else if (s < s1)
+          batch(s, std::true_type{}, B4{});
 #pragma unroll
         for (int u = 0; u < NS; ++u)
 #pragma unroll
@@ -2670,7 +2725,9 @@ static int contrastive_backward_impl(
       ba.parts = parts;
       ba.part_slices = g2;
       ba.group = g2;
+      // the row order reuses the cursor array: kBkClasses + R / 2 <= R + 1
       ba.rows_per_pass = 1024;
+      static_assert(kBkClasses + 1024 / 2 <= 1024 + 1, "row order does not fit the cursor array");
       ba.entries_per_pass = (int)ne_all;
       const size_t blds = 2 * (size_t)(ba.rows_per_pass + 1) * sizeof(int) +
                           ((size_t)ne_all + (size_t)num_queries) * sizeof(int);
