@@ -654,6 +654,12 @@ def main():
 
         ms2 = time_wall(torch, step2, K, W)
 
+        # loss and gradients in one call, without the autograd engine
+        def step2_vg():
+            maxsim_amd.score_contrastive_cross_entropy_value_and_grad(q2, d2, off2)
+
+        ms2_vg = time_wall(torch, step2_vg, K, W)
+
         def step2_fused():
             q2g.grad = None
             d2g.grad = None
@@ -664,6 +670,7 @@ def main():
         with maxsim_amd.host_checks(False):
             ms2_nowait = time_wall(torch, step2, K, W)
             ms2_fused_nowait = time_wall(torch, step2_fused, K, W)
+            ms2_vg_nowait = time_wall(torch, step2_vg, K, W)
             # the same step captured once in a HIP graph and replayed
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -683,10 +690,13 @@ def main():
         extra["c2"] = {"step_ms": round(ms2, 4),
                        "no_host_checks_step_ms": round(ms2_nowait, 4),
                        "fused_ce_no_host_checks_step_ms": round(ms2_fused_nowait, 4),
+                       "value_and_grad_step_ms": round(ms2_vg, 4),
+                       "value_and_grad_no_host_checks_step_ms": round(ms2_vg_nowait, 4),
                        "graph_step_ms": round(ms2_graph, 4),
                        "fwd_ms": round(time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(q2, d2, off2), K, 2), 4)}
         log(f"C2: step {ms2:.4f} ms; host checks off {ms2_nowait:.4f} ms, fused "
-            f"{ms2_fused_nowait:.4f} ms, graph {ms2_graph:.4f} ms")
+            f"{ms2_fused_nowait:.4f} ms, graph {ms2_graph:.4f} ms, value_and_grad "
+            f"{ms2_vg:.4f} ms ({ms2_vg_nowait:.4f} ms host checks off)")
 
         # ---------------- C3: padded rerank docs/s ----------------
         log("C3: padded rerank 256x1000 (19.7 GB fp16)")

@@ -30,6 +30,7 @@ from maxsim_amd import (  # noqa: F401  (re-exported)
     score_contrastive,
     score_contrastive_backward_reference,
     score_contrastive_cross_entropy,
+    score_contrastive_cross_entropy_value_and_grad,
     score_contrastive_reference,
     score_contrastive_train,
     score_contrastive_with_argmax,

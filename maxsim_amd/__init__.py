@@ -875,27 +875,10 @@ class _ContrastiveCEFn(torch.autograd.Function):
         return dq, dd, None, None, None, None
 
 
-def score_contrastive_cross_entropy(queries, documents, document_offsets, targets=None, *,
-                                    temperature: float = 1.0,
-                                    reduction: str = "mean") -> torch.Tensor:
-    """The contrastive training loss in one call:
-    ``F.cross_entropy(score_contrastive_train(queries, documents,
-    document_offsets) / temperature, targets, reduction=reduction)``, the
-    recipe of the reference's README (README.md:193-205), with the softmax
-    gradient fused into the backward kernels.
-
-    Args:
-        queries, documents, document_offsets: as :func:`score_contrastive`.
-        targets: ``[Nq]`` int32/int64 class (document) per query, or None for
-            the diagonal (query i's positive is document i; needs Nq <= Nb).
-        temperature: the scores are divided by it (> 0).
-        reduction: ``"mean"`` (default), ``"sum"`` or ``"none"`` (``[Nq]``).
-
-    Returns:
-        fp32 loss (0-dim, or ``[Nq]`` for ``"none"``); differentiable with
-        respect to queries and documents (gradients in their dtype).  Not in
-        the reference's ``__all__``; its users call torch's cross-entropy.
-    """
+def _check_cross_entropy(queries, documents, document_offsets, targets, temperature,
+                         reduction):
+    """Argument checks of the fused contrastive cross-entropy; returns
+    ``(1 / temperature, reduction code)``."""
     _check_contrastive(queries, documents, document_offsets)
     if reduction not in _REDUCTIONS:
         raise ValueError(f"reduction must be 'mean', 'sum' or 'none'; got {reduction!r}")
@@ -918,7 +901,87 @@ def score_contrastive_cross_entropy(queries, documents, document_offsets, target
             if bad.size:
                 i = int(bad[0])
                 raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {Nb})")
+    return 1.0 / temperature, _REDUCTIONS[reduction]
+
+
+def score_contrastive_cross_entropy(queries, documents, document_offsets, targets=None, *,
+                                    temperature: float = 1.0,
+                                    reduction: str = "mean") -> torch.Tensor:
+    """The contrastive training loss in one call:
+    ``F.cross_entropy(score_contrastive_train(queries, documents,
+    document_offsets) / temperature, targets, reduction=reduction)``, the
+    recipe of the reference's README (README.md:193-205), with the softmax
+    gradient fused into the backward kernels.
+
+    Args:
+        queries, documents, document_offsets: as :func:`score_contrastive`.
+        targets: ``[Nq]`` int32/int64 class (document) per query, or None for
+            the diagonal (query i's positive is document i; needs Nq <= Nb).
+        temperature: the scores are divided by it (> 0).
+        reduction: ``"mean"`` (default), ``"sum"`` or ``"none"`` (``[Nq]``).
+
+    Returns:
+        fp32 loss (0-dim, or ``[Nq]`` for ``"none"``); differentiable with
+        respect to queries and documents (gradients in their dtype).  Not in
+        the reference's ``__all__``; its users call torch's cross-entropy.
+    """
+    inv_t, red = _check_cross_entropy(queries, documents, document_offsets, targets,
+                                      temperature, reduction)
     return _checked_contrastive(
         queries, documents, document_offsets,
-        lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets,
-                                       1.0 / temperature, _REDUCTIONS[reduction]))
+        lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets, inv_t, red))
+
+
+def score_contrastive_cross_entropy_value_and_grad(queries, documents, document_offsets,
+                                                   targets=None, *, temperature: float = 1.0,
+                                                   reduction: str = "mean", grad_loss=None):
+    """:func:`score_contrastive_cross_entropy` and its gradients in one call,
+    without autograd: returns ``(loss, dqueries, ddocuments)``.
+
+    The same kernels as ``score_contrastive_cross_entropy(...).backward()``
+    (forward with argmax, the loss with each row's log-sum-exp, the fused
+    backward), launched back to back.  The autograd engine's per-backward
+    host cost (a thread hand-off and graph walk, tens of microseconds) is
+    larger than all the kernels of a small batch; training loops that apply
+    the gradients themselves avoid it here.
+
+    Args:
+        queries, documents, document_offsets, targets, temperature,
+            reduction: as :func:`score_contrastive_cross_entropy`
+            (``requires_grad`` is ignored; nothing is recorded).
+        grad_loss: upstream gradient of the loss, fp32 on the inputs' device:
+            one value (``"mean"``/``"sum"``) or ``[Nq]`` (``"none"``); None
+            means 1 (``[Nq]`` ones for ``"none"``).
+
+    Returns:
+        ``loss`` (fp32, 0-dim or ``[Nq]``) and the gradients of
+        ``(loss * grad_loss).sum()`` with respect to queries and documents,
+        in their dtype (fp32 sums rounded once).
+    """
+    inv_t, red = _check_cross_entropy(queries, documents, document_offsets, targets,
+                                      temperature, reduction)
+    nq = queries.shape[0]
+    if grad_loss is not None:
+        if not isinstance(grad_loss, torch.Tensor) or grad_loss.dtype != torch.float32:
+            raise TypeError("grad_loss must be a float32 tensor")
+        _require_one_device(queries=queries, grad_loss=grad_loss)
+        want = nq if reduction == "none" else 1
+        if grad_loss.numel() != want:
+            raise ValueError(f"grad_loss must hold {want} value(s); got {grad_loss.numel()}")
+
+    def launch():
+        q, d = queries.detach().contiguous(), documents.detach().contiguous()
+        offs = document_offsets.to(torch.int32).contiguous()
+        scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, offs)
+        tgt = None if targets is None else targets.to(torch.int32).contiguous()
+        lse, loss = ops.maxsim_cross_entropy_forward(scores, tgt, inv_t, red)
+        g = grad_loss
+        if g is None:
+            g = torch.ones(loss.shape, dtype=torch.float32, device=loss.device)
+        dq, dd = ops.maxsim_contrastive_cross_entropy_backward(
+            g.detach().reshape(loss.shape).contiguous(), scores, lse, tgt, inv_t, red, q, d,
+            offs, argmax)
+        return loss, dq, dd
+
+    with torch.no_grad():
+        return _checked_contrastive(queries, documents, document_offsets, launch)

@@ -251,6 +251,27 @@ def test_cross_entropy_validation():
         maxsim_amd.score_contrastive_cross_entropy(q5, d5, off5)
 
 
+def test_value_and_grad_validation():
+    """score_contrastive_cross_entropy_value_and_grad shares the loss's
+    argument checks and checks grad_loss; CPU tensors fail loudly."""
+    q, d, off = _contrastive(Nq=3, Nb=4)
+    vg = maxsim_amd.score_contrastive_cross_entropy_value_and_grad
+    with pytest.raises(ValueError, match="reduction"):
+        vg(q, d, off, reduction="avg")
+    with pytest.raises(ValueError, match="out of range"):
+        vg(q, d, off, torch.tensor([0, 1, 4]))
+    with pytest.raises(TypeError, match="grad_loss"):
+        vg(q, d, off, grad_loss=torch.ones((), dtype=torch.float64))
+    with pytest.raises(ValueError, match="grad_loss"):
+        vg(q, d, off, grad_loss=torch.ones(3))
+    with pytest.raises(ValueError, match="grad_loss"):
+        vg(q, d, off, reduction="none", grad_loss=torch.ones(()))
+    with pytest.raises(NotImplementedError):
+        vg(q, d, off)
+    import maxsim
+    assert maxsim.score_contrastive_cross_entropy_value_and_grad is vg
+
+
 def test_host_checks_switch():
     """set_host_checks / host_checks toggle the process-wide setting and
     restore it; with checks off, shape and dtype errors still raise, and

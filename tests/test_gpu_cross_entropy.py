@@ -139,3 +139,54 @@ def test_fused_ops_match_dscore_path():
                                                            off, argmax)
     assert_close(dq, dq_ref.cpu().numpy(), rtol=1e-2, atol=1e-5)
     assert_close(dd, dd_ref.cpu().numpy(), rtol=1e-2, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=lambda t: _ids[t])
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_value_and_grad_vs_autograd_and_oracle(reduction, dtype):
+    """score_contrastive_cross_entropy_value_and_grad gives the autograd
+    path's loss and gradients (the same kernels: loss and dQ bit for bit, dD
+    up to the order of its bucket sums) and the oracle's."""
+    Nq, Lq, dim, d_lens = 8, 32, 128, [40, 300, 17, 64, 128, 9, 255, 77, 31, 500]
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=11, unit=True)
+    gen = torch.Generator().manual_seed(5)
+    targets = torch.randint(0, len(d_lens), (Nq,), generator=gen).to(DEVICE)
+    upstream = torch.randn(Nq, generator=gen).to(DEVICE) if reduction == "none" else None
+    kw = dict(temperature=0.1, reduction=reduction)
+    loss, dq, dd = maxsim_amd.score_contrastive_cross_entropy_value_and_grad(
+        q, d, off, targets, grad_loss=upstream, **kw)
+    assert loss.shape == ((Nq,) if reduction == "none" else ())
+    assert dq.dtype == dtype and dd.dtype == dtype and dq.shape == q.shape
+    qg, dg = q.clone().requires_grad_(True), d.clone().requires_grad_(True)
+    ref = maxsim_amd.score_contrastive_cross_entropy(qg, dg, off, targets, **kw)
+    ref.backward(upstream)
+    assert torch.equal(loss, ref.detach())
+    assert torch.equal(dq, qg.grad)
+    # dD rows add their bucket in LDS-atomic order: fp32 rounding apart
+    # (or one bfloat16 step after rounding)
+    scale = float(dg.grad.float().abs().max())
+    torch.testing.assert_close(dd, dg.grad, rtol=1e-5 if dtype == torch.float32 else 8e-3,
+                               atol=1e-6 * scale)
+    l_ref, dq_ref, dd_ref = _oracle(q, d, off, targets, 10.0, reduction, upstream)
+    assert_close(loss, l_ref, rtol=1e-4 if dtype == torch.float32 else 2e-4, atol=1e-4)
+    tol = GRAD_TOL[dtype] if dtype == torch.float32 else dict(rtol=1e-2, atol=2e-3)
+    assert_close(dq, dq_ref, **tol)
+    assert_close(dd, dd_ref, **tol)
+
+
+def test_value_and_grad_default_diagonal_and_no_graph():
+    """Diagonal targets and grad_loss None (= 1); inputs that require grad
+    get no autograd graph and no .grad."""
+    q, d, off = make_contrastive(6, 32, 64, [50, 20, 90, 33, 70, 12, 8], torch.bfloat16, seed=2,
+                                 unit=True)
+    qg, dg = q.clone().requires_grad_(True), d.clone().requires_grad_(True)
+    loss, dq, dd = maxsim_amd.score_contrastive_cross_entropy_value_and_grad(qg, dg, off)
+    assert loss.grad_fn is None and not dq.requires_grad and qg.grad is None
+    l2, dq2, dd2 = maxsim_amd.score_contrastive_cross_entropy_value_and_grad(
+        q, d, off, grad_loss=torch.full((), 2.0, device=DEVICE))
+    assert torch.equal(l2, loss)
+    l_ref, dq_ref, dd_ref = _oracle(q, d, off, None, 1.0, "mean")
+    assert_close(loss, l_ref, rtol=2e-4, atol=1e-4)
+    assert_close(dq, dq_ref, rtol=1e-2, atol=2e-3)
+    assert_close(dd, dd_ref, rtol=1e-2, atol=2e-3)
+    assert_close(dq2, 2 * dq_ref, rtol=1e-2, atol=4e-3)
