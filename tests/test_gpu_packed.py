@@ -376,3 +376,28 @@ def test_packed_validation_sees_writes_queued_just_before():
     with pytest.raises(RuntimeError, match="pair_document_ids"):
         maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids, max_q_len=20)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("host_checks", [True, False], ids=["checks", "no-checks"])
+def test_score_only_beyond_2pow20_query_rows(host_checks):
+    """A score-only call without max_q_len over more than 2^20 query rows
+    (four segments of 250k-300k tokens, fp32, dim 8) gives the oracle's
+    scores: its query-length bound is the row count, and only the argmax
+    shape is capped at 2^20 slots."""
+    gen = torch.Generator().manual_seed(21)
+    q_lens, d_lens, dim = [300_000, 250_000, 275_000, 275_000], [3, 17, 40, 8, 25], 8
+    q = torch.randn(sum(q_lens), dim, generator=gen)
+    q = (q / q.norm(dim=1, keepdim=True)).to(DEVICE)
+    d = torch.randn(sum(d_lens), dim, generator=gen)
+    d = (d / d.norm(dim=1, keepdim=True)).to(DEVICE)
+    qoff = offsets_from_lengths(q_lens).to(DEVICE)
+    doff = offsets_from_lengths(d_lens).to(DEVICE)
+    qids = torch.tensor([0, 1, 2, 3, 0, 3], dtype=torch.int32, device=DEVICE)
+    dids = torch.tensor([0, 2, 4, 1, 3, 3], dtype=torch.int32, device=DEVICE)
+    assert q.shape[0] > (1 << 20)
+    with maxsim_amd.host_checks(host_checks):
+        s = maxsim_amd.score_pairs_packed(q, qoff, d, doff, qids, dids)
+    s_ref, _ = oracle.packed_forward(np64(q), npi(qoff), np64(d), npi(doff), npi(qids),
+                                     npi(dids), max(q_lens))
+    # sums of 250k-300k token maxima in fp32 (a few 1e-6 relative)
+    assert_close(s, s_ref, rtol=5e-5, atol=1e-2)
