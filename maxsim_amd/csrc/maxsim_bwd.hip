@@ -1951,8 +1951,9 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
           if (start[rr + 1] > start[rr]) cursor[atomicAdd(&n_full, 1)] = rr;
         if (first) {
           const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          const float inv_sl = 1.0f / (float)sl_hi;
           for (int x = tid; x < nrows * sl_hi; x += kGroupThreads) {
-            const int rr = x / sl_hi;
+            const int rr = div_small(x, sl_hi, inv_sl);
             if (start[rr + 1] == start[rr])
               store8<O>(out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim), (x - rr * sl_hi) * 8, dim,
                         VEC, zero8);
@@ -1985,36 +1986,48 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
             for (int u = 0; u < NS; ++u)
 #pragma unroll
               for (int x = 0; x < 8; ++x) blk[u][x] = 0.0f;
-            for (int s = s0; s < s1; s += kDdBatch) {
-              const S* row[kDdBatch];
-              float gx[kDdBatch];
-              bool ok[kDdBatch];
+            // KB entries from s; past the bucket's end (masked batches only)
+            // an entry repeats entry s with its fragment and weight zeroed
+            // (fmaf(0, 0, x) == x exactly).  Full batches of kDdBatch while
+            // they last, then pairs: most rows of a sparse document hold one
+            // or two entries.
+            auto batch = [&](int s, auto masked, auto kb) {
+              constexpr bool MASKED = decltype(masked)::value;
+              constexpr int KB = decltype(kb)::value;
+              const S* row[KB];
+              float gx[KB];
+              bool ok[KB];
 #pragma unroll
-              for (int k = 0; k < kDdBatch; ++k) {
-                ok[k] = s + k < s1;
+              for (int k = 0; k < KB; ++k) {
+                ok[k] = !MASKED || s + k < s1;
                 const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
                 const int kk = (int)(v >> 16);
                 const int i = t0 + (int)(v & 0xffffu) - kk * tc;
                 row[k] = Q + (st_qs[kk] + i) * (int64_t)dim;
-                gx[k] = st_g[kk];
+                gx[k] = ok[k] ? st_g[kk] : 0.0f;
               }
 #pragma unroll
               for (int u = 0; u < NS; ++u) {
                 const int sl = sc + gl + u * G;
                 if (sl < sl_hi) {
-                  Frag<T> v[kDdBatch];
+                  Frag<T> v[KB];
 #pragma unroll
-                  for (int k = 0; k < kDdBatch; ++k) v[k] = load_frag<T>(row[k], sl * 8, dim, VEC);
+                  for (int k = 0; k < KB; ++k) {
+                    v[k] = load_frag<T>(row[k], sl * 8, dim, VEC);
+                    if (MASKED && !ok[k]) v[k] = zero_frag<T>();
+                  }
 #pragma unroll
-                  for (int k = 0; k < kDdBatch; ++k)
+                  for (int k = 0; k < KB; ++k)
 #pragma unroll
-                    for (int x = 0; x < 8; ++x) {
-                      const float t = fmaf(gx[k], frag_elem(v[k], x), blk[u][x]);
-                      blk[u][x] = ok[k] ? t : blk[u][x];
-                    }
+                    for (int x = 0; x < 8; ++x)
+                      blk[u][x] = fmaf(gx[k], frag_elem(v[k], x), blk[u][x]);
                 }
               }
-            }
+            };
+            int s = s0;
+            for (; s + kDdBatch <= s1; s += kDdBatch)
+              batch(s, std::false_type{}, std::integral_constant<int, kDdBatch>{});
+            for (; s < s1; s += 2) batch(s, std::true_type{}, std::integral_constant<int, 2>{});
 #pragma unroll
             for (int u = 0; u < NS; ++u)
 #pragma unroll
