@@ -803,6 +803,11 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
 // the tile loads: twice the tiles in flight per wave, at no register cost
 // (the staging registers are freed).  The load stream runs across pairs:
 // the next pair's first tiles load during the current pair's last ones.
+// Vector-memory operations complete in order, so any other load would make
+// its wait a wait for every tile load before it: a pair's query blocks come
+// through the same stream (a query block is a 32-row tile of the same
+// layout, read into the B fragments), and the wave's pair metadata is
+// resolved once, one pair per lane, and read back with readlane.
 // No barriers: each wave owns its slots.  Same MFMA order and tile epilogue
 // as pair_kernel, so the results are bit-identical.
 // ---------------------------------------------------------------------------
@@ -840,17 +845,46 @@ __global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, i
 #pragma unroll
   for (int s = 0; s < KS; ++s) aoff[s] = c * G::P + ((2 * s + h) ^ (c & G::SWZ));
 
-  // ---- load stream: the valid pairs' tiles in order
-  int64_t lp = p_begin;
-  Pair lpr = resolve_pair(a, lp);
-  while (!lpr.ok && ++lp < p_end) lpr = resolve_pair(a, lp);
-  int lt = 0;
-  int issued = 0;  // stream tiles whose loads were issued
+  // ---- pair metadata: lane i resolves pair p_begin + i once (ppw <= 64,
+  // the host's bound), and the walks below read it back with readlane, so
+  // no metadata load sits between the tile loads in flight and their waits
+  // (vector-memory operations complete in order: waiting for such a load
+  // would wait for every tile load issued before it)
+  const int npw = (int)(p_end - p_begin);
+  Pair mine{0, 0, 0, 0, false};
+  if (lane < npw) mine = resolve_pair(a, p_begin + lane);
+  auto pair_at = [&](int i) __attribute__((always_inline)) {
+    Pair r;
+    const uint32_t qlo = __builtin_amdgcn_readlane((int)(uint32_t)mine.q_row0, i);
+    const uint32_t qhi = __builtin_amdgcn_readlane((int)(mine.q_row0 >> 32), i);
+    const uint32_t dlo = __builtin_amdgcn_readlane((int)(uint32_t)mine.d_row0, i);
+    const uint32_t dhi = __builtin_amdgcn_readlane((int)(mine.d_row0 >> 32), i);
+    r.q_row0 = (int64_t)(((uint64_t)qhi << 32) | qlo);
+    r.d_row0 = (int64_t)(((uint64_t)dhi << 32) | dlo);
+    r.lq = __builtin_amdgcn_readlane(mine.lq, i);
+    r.ld = __builtin_amdgcn_readlane(mine.ld, i);
+    r.ok = __builtin_amdgcn_readlane(mine.ok ? 1 : 0, i) != 0;
+    return r;
+  };
+
+  // ---- load stream: for each valid pair in order, its query blocks (32
+  // token rows each, the B operands), then its document tiles; each unit is
+  // one 32-row tile of 16-byte pieces, swizzled alike, in the next slot
+  int li = 0;        // pair of the next unit
+  int lu = 0;        // unit within that pair
+  Pair lpr = pair_at(0);
+  while (!lpr.ok && ++li < npw) lpr = pair_at(li);
+  int issued = 0;    // units whose loads were issued
   auto dma_next = [&]() __attribute__((always_inline)) {
-    if (lp >= p_end) return;
+    if (li >= npw) return;
     const int slot = issued % kRingSlots;
-    const S* base = D + (lpr.d_row0 + (int64_t)lt * kTileRows) * dim;
-    const int last = lpr.ld - 1 - lt * kTileRows;
+    const int nblk = (lpr.lq + kTileCols - 1) / kTileCols;
+    const int ntiles = (lpr.ld + kTileRows - 1) / kTileRows;
+    const bool isq = lu < nblk;
+    const int t = isq ? lu : lu - nblk;
+    const S* base = isq ? Q + (lpr.q_row0 + (int64_t)t * kTileCols) * dim
+                        : D + (lpr.d_row0 + (int64_t)t * kTileRows) * dim;
+    const int last = (isq ? lpr.lq : lpr.ld) - 1 - t * kTileRows;
 #pragma unroll
     for (int i = 0; i < kDma; ++i) {
       const int r = i * kRPI + l_hi;
@@ -859,14 +893,14 @@ __global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, i
       lds_dma16(base, off, ring_lds + (uint32_t)((slot * G::kBufPieces + i * 64) * sizeof(uint4)));
     }
     ++issued;
-    if (++lt * kTileRows >= lpr.ld) {
-      lt = 0;
+    if (++lu >= nblk + ntiles) {
+      lu = 0;
       do {
-        ++lp;
-      } while (lp < p_end && !(lpr = resolve_pair(a, lp)).ok);
+        ++li;
+      } while (li < npw && !(lpr = pair_at(li)).ok);
     }
   };
-  // s_waitcnt vmcnt(n), n = kDma (the next tile's loads may be outstanding) or 0
+  // s_waitcnt vmcnt(n), n = kDma (the next unit's loads may be outstanding) or 0
   auto wait_tile = [&](bool next_issued) __attribute__((always_inline)) {
     if (next_issued) {
       if constexpr (kDma == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
@@ -878,26 +912,39 @@ __global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, i
     }
     __asm__ __volatile__("" ::: "memory");
   };
+  // the unit's slot has been read into registers: refill it with the unit
+  // two ahead (lgkmcnt(0): the reads have completed)
+  auto refill = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __asm__ __volatile__("" ::: "memory");
+    dma_next();
+  };
   dma_next();
   dma_next();
 
   Frag<T> qf[QB][KS];
-  int k = 0;  // stream index of the tile being computed
-  for (int64_t p = p_begin; p < p_end; ++p) {
-    const Pair pr = resolve_pair(a, p);
+  int k = 0;  // stream index of the unit being consumed
+  for (int i = 0; i < npw; ++i) {
+    const int64_t p = p_begin + i;
+    const Pair pr = pair_at(i);
     if (!pr.ok) {
       write_invalid_pair(a, p, lane);
       continue;
     }
     const int nblk = (pr.lq + kTileCols - 1) / kTileCols;  // <= QB (host checks)
     const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
+    // query blocks from the stream: the same layout as a document tile, so
+    // lane c reads token c's fragments (rows past the query end repeat its
+    // last token, as the register loads did)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       if (qb >= nblk) break;
-      const int tok = min(qb * kTileCols + c, pr.lq - 1);
-      const S* row = Q + (pr.q_row0 + tok) * (int64_t)dim;
+      wait_tile(issued > k + 1);
+      const uint4* tile = ring + (k % kRingSlots) * G::kBufPieces;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) qf[qb][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, true);
+      for (int s = 0; s < KS; ++s) qf[qb][s].v = tile[aoff[s]];
+      ++k;
+      refill();
     }
     float m[QB];
     int am[QB];
@@ -921,11 +968,7 @@ __global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, i
 #pragma unroll
           for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
         }
-        // the slot's fragments are in registers: refill it with the tile two
-        // ahead (lgkmcnt(0): the reads have completed)
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __asm__ __volatile__("" ::: "memory");
-        dma_next();
+        refill();
 #pragma unroll
         for (int qb = 0; qb < NA; ++qb)
           tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
