@@ -40,7 +40,7 @@ PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 # build's own pack_rows_kernel copying 1 GiB: FETCH x1.997, WRITE x1.000).
 # Counters cannot be read from inside this process, so the figure is the
 # committed measurement, not a live one.
-FWD_TRAFFIC_BYTES_C5 = int((52934.7 * 1.997 + 33888.9 * 1.000) * 1024)
+FWD_TRAFFIC_BYTES_C5 = int((52939.0 * 1.997 + 33888.4 * 1.000) * 1024)
 
 
 def parse_args():
@@ -618,15 +618,19 @@ def main():
     # One GPU's shard of C5 split by query rows over 8 GPUs (64 of the 512
     # queries against all 512 documents): the kernels at the shape each rank
     # would run, without the collectives (one GPU here).
-    qs = q[:64].contiguous()
-    ms_sf = time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(qs, d, off), K, 2)
-    s_s, a_s = ops.maxsim_contrastive_forward_with_argmax(qs, d, off)
-    g_s = dscore[:64].contiguous()
-    ms_sb = time_events(torch, lambda: ops.maxsim_contrastive_backward_typed(g_s, qs, d, off, a_s), K, 2)
-    extra["c5_shard_of_8"] = {"Nq": 64, "Nb": nb, "fwd_ms": round(ms_sf, 4),
-                              "fwd_tflops": round(flops_fwd / 8 / (ms_sf * 1e-3) / 1e12, 2),
-                              "bwd_typed_ms": round(ms_sb, 4)}
-    del s_s, a_s
+    # (not in --quick, whose kernel trace averages the full-size C5 forward)
+    if not args.quick:
+        qs = q[:64].contiguous()
+        ms_sf = time_events(torch, lambda: ops.maxsim_contrastive_forward_with_argmax(qs, d, off),
+                            K, 2)
+        s_s, a_s = ops.maxsim_contrastive_forward_with_argmax(qs, d, off)
+        g_s = dscore[:64].contiguous()
+        ms_sb = time_events(torch, lambda: ops.maxsim_contrastive_backward_typed(
+            g_s, qs, d, off, a_s), K, 2)
+        extra["c5_shard_of_8"] = {"Nq": 64, "Nb": nb, "fwd_ms": round(ms_sf, 4),
+                                  "fwd_tflops": round(flops_fwd / 8 / (ms_sf * 1e-3) / 1e12, 2),
+                                  "bwd_typed_ms": round(ms_sb, 4)}
+        del s_s, a_s
 
     if not args.quick:
         # ---------------- C1: small padded rerank, fp32 ----------------
