@@ -383,3 +383,38 @@ def test_contrastive_validation_sees_writes_queued_just_before():
     with pytest.raises(ValueError):
         maxsim_amd.score_contrastive(q, d, off)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_contrastive_backward_skewed_buckets(dtype):
+    """Document 0 holds a large row v and its negation -v: nearly every
+    query token picks one of the two (|<v, q>| dominates), so two rows of
+    document 0 receive almost all of its 5120 entries (far above the largest row size class
+    of the dD row order, which documents of >= 4096 entries use) and its
+    other rows none.  fp32 and typed gradients against the oracle; the typed
+    ones are the fp32 ones rounded."""
+    Nq, Lq, dim, d_lens = 160, 32, 128, [300, 40, 128, 700]
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=29)
+    v = torch.randn(dim, generator=torch.Generator().manual_seed(30)) * 100
+    d[5] = v.to(dtype).to(DEVICE)
+    d[6] = (-v).to(dtype).to(DEVICE)
+    gen = torch.Generator().manual_seed(31)
+    dscore = torch.randn(Nq, len(d_lens), generator=gen).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    a0 = argmax[:, 0, :]
+    assert float(((a0 == 5) | (a0 == 6)).float().mean()) > 0.9  # tokens almost orthogonal to v
+    picked = torch.zeros(d_lens[0], dtype=torch.bool, device=DEVICE)
+    picked[a0.reshape(-1).long()] = True
+    dq, dd = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off),
+                                                 npi(argmax))
+    tol = GRAD_TOL[dtype]
+    assert_close(dq, dq_ref, **tol)
+    # the two hot rows sum ~2560 terms each: tolerance scaled by their size
+    assert_close(dd, dd_ref, rtol=tol["rtol"], atol=tol["atol"] * 50)
+    assert bool((dd[:d_lens[0]][~picked] == 0).all())  # rows no entry picked
+    if dtype != torch.float32:
+        dqt, ddt = ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+        assert torch.equal(dqt, dq.to(dtype))
+        _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
+        assert_rounded_from(ddt, dd, mag)
