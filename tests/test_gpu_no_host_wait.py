@@ -198,3 +198,33 @@ def test_c2_training_step_captured_in_a_graph(no_checks, fused):
         torch.testing.assert_close(static_dd.float(), eager_dd.float(), rtol=1e-2, atol=1e-6)
         # eager work between replays
         maxsim_amd.score_contrastive(q, d, off).sum().item()
+
+
+def test_c2_value_and_grad_captured_in_a_graph(no_checks):
+    """score_contrastive_cross_entropy_value_and_grad (no autograd) captured
+    in a HIP graph at C2: each replay, with eager work and synchronisations
+    between replays, gives the eager call's loss and dQ bit for bit and dD
+    up to its bucket-sum order."""
+    q, d, off, _ = _c2_inputs()
+    vg = maxsim_amd.score_contrastive_cross_entropy_value_and_grad
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            vg(q, d, off)
+    torch.cuda.current_stream().wait_stream(side)
+    eager = [t.clone() for t in vg(q, d, off)]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = vg(q, d, off)
+    for r in range(4):
+        for t in static:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _same(static[0], eager[0])
+        _same(static[1], eager[1])
+        torch.testing.assert_close(static[2].float(), eager[2].float(), rtol=1e-2, atol=1e-6)
+        # eager work between replays
+        maxsim_amd.score_contrastive(q, d, off).sum().item()
