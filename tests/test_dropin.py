@@ -3,7 +3,8 @@
 The reference's callers write ``import maxsim`` and ``from maxsim._ops import
 ops`` (reference tests/conftest.py:129-145, tests/test_backward.py:15-16);
 ``maxsim`` here is a thin package over ``maxsim_amd``.  Also checks that the
-ABI version INTEGRATION.md documents is the one the library reports."""
+ABI version the integration guide at the repository root states is the one
+the library reports."""
 
 from __future__ import annotations
 
