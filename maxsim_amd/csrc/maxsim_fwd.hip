@@ -1112,11 +1112,11 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
   // the LDS-ring variant (two tiles in flight per wave)
   if (dtype != MAXSIM_FLOAT32 && vec && ks_for_dim(a.dim) <= 8 && max_lq <= 2 * kTileCols &&
       a.mode != kContrastive) {
-    // Above 32k pairs the ring aims for ~32k waves instead of ~16k (C3:
-    // 8 pairs per wave, 1.79 against 1.82 ms); below, two pairs per wave
-    // stay better than one (C4: 195 against 203-206 us).
-    const int ppw_r = a.npairs > 32768 ? (int)std::min<int64_t>((a.npairs + 32767) / 32768, 64)
-                                       : ppw;
+    // Above 32k pairs the ring takes one pair per wave (C3, 256k pairs:
+    // 1.74 ms, against 1.75 / 1.77 / 1.78 / 1.83 ms at 2 / 4 / 8 / 16 pairs
+    // per wave); below, the ~16k-wave rule (C4: 2 pairs per wave, 195 us,
+    // against 203-206 us at one).
+    const int ppw_r = a.npairs > 32768 ? 1 : ppw;
     const int64_t waves = (a.npairs + ppw_r - 1) / ppw_r;
     const dim3 grid((unsigned)((waves + kRingWaves - 1) / kRingWaves));
     switch (dtype) {
