@@ -13,9 +13,13 @@
 
 namespace maxsim {
 
-constexpr int kPackThreads = 256;
-constexpr int64_t kPackChunk = 65536;  // bytes per workgroup
-constexpr int kPackUnroll = 4;         // copy units in flight per thread
+// 1024 threads x 4 units in flight x 16 B = 64 KB per pass, two passes per
+// workgroup: at the 256k-document shape this copies at ~5.7 TB/s, against
+// ~5.1 TB/s with 256 threads and 64 KB chunks (and ~4.9 TB/s for a plain
+// device-to-device tensor copy of the same size).
+constexpr int kPackThreads = 1024;
+constexpr int64_t kPackChunk = 131072;  // bytes per workgroup
+constexpr int kPackUnroll = 4;          // copy units in flight per thread
 
 struct PackArgs {
   const char* src;
@@ -27,7 +31,7 @@ struct PackArgs {
   int64_t dst_rows;
 };
 
-// Workgroup = (segment, 64 KB chunk of its valid bytes); V is the copy unit
+// Workgroup = (segment, 128 KB chunk of its valid bytes); V is the copy unit
 // (16, 8, 4 or 2 bytes), which divides the row size and both base addresses.
 template <typename V>
 __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(PackArgs a) {
