@@ -332,8 +332,8 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 // Range r = w % kXcds of the documents is therefore gathered only by the
 // workgroups of one XCD, so each XCD's L2 serves 1/8 of D instead of all of
 // it.  A thread owns (query row, 8-element slice, range) and writes its fp32
-// partial sum to ws[range]; dq_reduce_kernel adds the kXcds parts in range
-// order, so dq is bitwise reproducible.
+// partial sum to ws[range]; dq_reduce_kernel (or dd_bucket_kernel's fused
+// share) adds the kXcds parts in range order, so dq is bitwise reproducible.
 //
 // The workgroup's rows and a chunk of the range's documents form a table of
 // (source row, weight) pairs, built in LDS by one coalesced pass over the
@@ -572,7 +572,8 @@ __global__ __launch_bounds__(256) void dq_walk_kernel(DqArgs a, int rows_per_gro
 // waits on no HBM latency: per document a lane reads its rows' winners with
 // two 16-byte LDS reads and issues eight gathers whose addresses are one
 // multiply-add each.  The partial sums of range r go to ws[r];
-// dq_reduce_kernel adds the kXcds parts in range order.
+// dq_reduce_kernel, or dd_bucket_kernel's fused share, adds the kXcds parts
+// in range order.
 // ---------------------------------------------------------------------------
 constexpr int kRangeItems = 8;
 constexpr int kRangeTableInts = 8192;              // argmax entries staged per stage (32 KB)
@@ -703,16 +704,13 @@ void dq_range_kernel(DqArgs a, float* __restrict__ ws) {
   }
 }
 
-// dq[x] = sum over the kXcds partial buffers, in range order, written in
-// the output type O.
+// dq[x] = sum over the kXcds partial buffers of x, in range order, written
+// in the output type O (4 consecutive elements when vec).
 template <typename O>
-__global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict__ ws,
-                                                        void* __restrict__ dq,
-                                                        int64_t n, bool vec) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n4 = vec ? n / 4 : 0;
-  for (int64_t x = t0; x < n4; x += stride) {
+__device__ __forceinline__ void dq_reduce_unit(const float* __restrict__ ws,
+                                               void* __restrict__ dq, int64_t n, bool vec,
+                                               int64_t x) {
+  if (vec) {
     float4 s = reinterpret_cast<const float4*>(ws)[x];
 #pragma unroll
     for (int r = 1; r < kXcds; ++r) {
@@ -726,8 +724,7 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict_
           make_uint2((uint32_t)to_out16<O>(s.x) | ((uint32_t)to_out16<O>(s.y) << 16),
                      (uint32_t)to_out16<O>(s.z) | ((uint32_t)to_out16<O>(s.w) << 16));
     }
-  }
-  for (int64_t x = n4 * 4 + t0; x < n; x += stride) {
+  } else {
     float s = ws[x];
 #pragma unroll
     for (int r = 1; r < kXcds; ++r) s += ws[r * n + x];
@@ -736,6 +733,19 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict_
     else
       static_cast<uint16_t*>(dq)[x] = to_out16<O>(s);
   }
+}
+
+// dq[x] = sum over the kXcds partial buffers, in range order, written in
+// the output type O.
+template <typename O>
+__global__ __launch_bounds__(256) void dq_reduce_kernel(const float* __restrict__ ws,
+                                                        void* __restrict__ dq,
+                                                        int64_t n, bool vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n4 = vec ? n / 4 : 0;
+  for (int64_t x = t0; x < n4; x += stride) dq_reduce_unit<O>(ws, dq, n, true, x);
+  for (int64_t x = n4 * 4 + t0; x < n; x += stride) dq_reduce_unit<O>(ws, dq, n, false, x);
 }
 
 // ---------------------------------------------------------------------------
@@ -777,6 +787,14 @@ struct DdArgs {
   int parts;             // dimension parts (1, 2, 4 or 8; divides kXcds)
   int part_slices;       // 8-element slices per part (last part may hold fewer)
   int group;             // lanes per row: power of two, <= 16, part_slices <= NS * group
+  // dd_bucket_kernel only: when dq_ws is set, each workgroup also adds its
+  // share of the kXcds dQ partial sums once its document is done (the work
+  // of dq_reduce_kernel, in the same order), so the memory-bound reduce
+  // overlaps the other workgroups' gathers instead of taking a launch.
+  const float* dq_ws;
+  void* dq_out;          // [dq_n] in the output type O
+  int64_t dq_n;
+  int dq_vec;            // dq_n % 4 == 0, dq_ws and dq_out 16-byte aligned
 };
 
 constexpr int kDdThreads = 512;
@@ -1039,7 +1057,7 @@ constexpr int kBkClasses = 256;        // row size classes: ceil(entries / 4), c
 constexpr int kBkOrderMin = 4096;      // entries per document from which rows are ordered
 
 template <typename T, int NS, typename O>
-__global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
+__device__ __forceinline__ void dd_bucket_document(DdArgs a) {
   using S = typename T::storage;
   extern __shared__ int lds_i[];
   const int R = a.rows_per_pass;
@@ -1284,6 +1302,29 @@ __global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
     }
     __syncthreads();
   }
+}
+
+// One document (and dimension part) per workgroup and, when the dQ reduce
+// is fused in, the workgroup's contiguous share of the reduce units (every
+// workgroup takes one, including those with no valid document).  The share
+// comes after the document for 16-bit gradients and before it for fp32 ones
+// (C5: 240 -> 233 us and 259 -> 253 us, against 240 -> 236 and 259 -> 258
+// the other way round; the dQ bits are the same either way).
+template <typename T, int NS, typename O>
+__global__ __launch_bounds__(kDdThreads) void dd_bucket_kernel(DdArgs a) {
+  auto reduce_share = [&]() {
+    const bool vec = a.dq_vec != 0;
+    const int64_t units = vec ? a.dq_n / 4 : a.dq_n;
+    const int64_t per = (units + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * per;
+    const int64_t hi = min(lo + per, units);
+    for (int64_t x = lo + threadIdx.x; x < hi; x += kDdThreads)
+      dq_reduce_unit<O>(a.dq_ws, a.dq_out, a.dq_n, vec, x);
+  };
+  constexpr bool kReduceFirst = O::bytes == 4;
+  if (kReduceFirst && a.dq_ws) reduce_share();
+  dd_bucket_document<T, NS, O>(a);
+  if (!kReduceFirst && a.dq_ws) reduce_share();
 }
 
 // ---------------------------------------------------------------------------
@@ -2215,7 +2256,7 @@ static void launch_dq_walk(const DqArgs& a, bool vec, bool off32, bool out16, hi
 // and D below 2 GiB (32-bit byte offsets); returns false otherwise.
 template <typename T>
 static bool launch_dq_range(const DqArgs& a, float* ws, bool vec, bool off32, bool vec_reduce,
-                            bool out16, hipStream_t st) {
+                            bool out16, bool reduce, hipStream_t st) {
   // fp32 fragments do not fit four waves per SIMD: dq_split_kernel takes fp32
   if constexpr (T::bytes == 4) {
     return false;
@@ -2237,6 +2278,7 @@ static bool launch_dq_range(const DqArgs& a, float* ws, bool vec, bool off32, bo
     case 32: hipLaunchKernelGGL((dq_range_kernel<T, 32>), grid, dim3(256), 0, st, a, ws); break;
     default: return false;
   }
+  if (!reduce) return true;  // the dD launch adds the partial sums
   const int64_t n = a.rows * a.dim;
   const int64_t work = vec_reduce ? n / 4 : n;
   const dim3 rgrid((unsigned)std::max<int64_t>(std::min<int64_t>((work + 255) / 256, 4096), 1));
@@ -2250,11 +2292,12 @@ static bool launch_dq_range(const DqArgs& a, float* ws, bool vec, bool off32, bo
 
 template <typename T>
 static void launch_dq_split(const DqArgs& a, bool vec, float* ws, bool vec_reduce, bool out16,
-                            hipStream_t st) {
+                            bool reduce, hipStream_t st) {
   const int rows_per_group = 256 / a.nslices;  // >= 8: dim <= 256
   const int64_t n_groups = (a.rows + rows_per_group - 1) / rows_per_group;
   hipLaunchKernelGGL((dq_split_kernel<T, kDqBatch>), dim3((unsigned)(n_groups * kXcds)),
                      dim3(256), 0, st, a, vec, ws, rows_per_group);
+  if (!reduce) return;  // the dD launch adds the partial sums
   const int64_t n = a.rows * a.dim;
   const int64_t work = vec_reduce ? n / 4 : n;
   const dim3 grid((unsigned)std::max<int64_t>(std::min<int64_t>((work + 255) / 256, 4096), 1));
@@ -2676,6 +2719,38 @@ static int contrastive_backward_impl(
                 (long long)(e_cap * Lq / (Lq + 1)));
   const size_t lds = bucket_bytes + ((size_t)da.entries_per_pass + (size_t)qpp) * sizeof(int);
 
+  // dd_bucket_kernel: every entry of a document in one pass, held 32 per
+  // thread, and parts of exactly 2 * G slices with G a power of two <= 16.
+  // Decided before dq, whose partial sums it can add (fused reduce).
+  bool bucket = false;
+  DdArgs ba = da;
+  size_t blds = 0;
+  {
+    const int64_t ne_all = num_queries * Lq;
+    // Few documents: more dimension parts (up to one per XCD), so that the
+    // launch has about two workgroups per CU; each part buckets its
+    // document's entries again, which costs little at such sizes.
+    int parts = da.parts;
+    while (parts < kXcds && num_documents * parts < 512 && nslices % (parts * 2) == 0)
+      parts *= 2;
+    const int g2 = nslices / parts;  // one slice per lane
+    if (vec && kDdThreads % Lq == 0 && g2 >= 1 && g2 <= kDdMaxGroup && (g2 & (g2 - 1)) == 0 &&
+        g2 * parts == nslices && ne_all <= (int64_t)kDdThreads * kBkMaxEntriesPerThread &&
+        q_bytes < ((int64_t)1 << 31) &&
+        num_queries * num_documents * Lq < ((int64_t)1 << 31)) {
+      ba.parts = parts;
+      ba.part_slices = g2;
+      ba.group = g2;
+      // the row order reuses the cursor array: kBkClasses + R / 2 <= R + 1
+      ba.rows_per_pass = 1024;
+      static_assert(kBkClasses + 1024 / 2 <= 1024 + 1, "row order does not fit the cursor array");
+      ba.entries_per_pass = (int)ne_all;
+      blds = 2 * (size_t)(ba.rows_per_pass + 1) * sizeof(int) +
+             ((size_t)ne_all + (size_t)num_queries) * sizeof(int);
+      bucket = blds <= max_lds_per_block();
+    }
+  }
+
   // dq
   DqArgs qa{};
   qa.ce = ce;
@@ -2702,12 +2777,18 @@ static int contrastive_backward_impl(
                             aligned16b(dqueries);
     bool done = false;
     switch (dtype) {
-      case MAXSIM_BFLOAT16: done = launch_dq_range<BF16>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
-      case MAXSIM_FLOAT16: done = launch_dq_range<F16>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
-      default: done = launch_dq_range<F32>(qa, ws, vec_ws, off32, vec_reduce, out16, st); break;
+      case MAXSIM_BFLOAT16: done = launch_dq_range<BF16>(qa, ws, vec_ws, off32, vec_reduce, out16, !bucket, st); break;
+      case MAXSIM_FLOAT16: done = launch_dq_range<F16>(qa, ws, vec_ws, off32, vec_reduce, out16, !bucket, st); break;
+      default: done = launch_dq_range<F32>(qa, ws, vec_ws, off32, vec_reduce, out16, !bucket, st); break;
     }
-    if (!done) MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, out16, st);
+    if (!done) MAXSIM_DISPATCH(dtype, launch_dq_split, qa, vec_ws, ws, vec_reduce, out16, !bucket, st);
     if (int e = check_launch("dq_range_kernel / dq_split_kernel")) return e;
+    if (bucket) {
+      ba.dq_ws = ws;
+      ba.dq_out = dqueries;
+      ba.dq_n = num_queries * Lq * dim;
+      ba.dq_vec = vec_reduce ? 1 : 0;
+    }
   } else if (nslices <= 256) {
     MAXSIM_DISPATCH(dtype, launch_dq_walk, qa, vec, off32, out16, st);
     if (int e = check_launch("dq_walk_kernel")) return e;
@@ -2716,39 +2797,9 @@ static int contrastive_backward_impl(
     if (int e = check_launch("dq_gather_kernel")) return e;
   }
 
-  // dd_bucket_kernel: every entry of a document in one pass, held 32 per
-  // thread, and parts of exactly 2 * G slices with G a power of two <= 16
-  {
-    const int64_t ne_all = num_queries * Lq;
-    // Few documents: more dimension parts (up to one per XCD), so that the
-    // launch has about two workgroups per CU; each part buckets its
-    // document's entries again, which costs little at such sizes.
-    int parts = da.parts;
-    while (parts < kXcds && num_documents * parts < 512 && nslices % (parts * 2) == 0)
-      parts *= 2;
-    const int g2 = nslices / parts;  // one slice per lane
-    const bool bucket = vec && kDdThreads % Lq == 0 && g2 >= 1 &&
-                        g2 <= kDdMaxGroup &&
-                        (g2 & (g2 - 1)) == 0 && g2 * parts == nslices &&
-                        ne_all <= (int64_t)kDdThreads * kBkMaxEntriesPerThread &&
-                        q_bytes < ((int64_t)1 << 31) &&
-                        num_queries * num_documents * Lq < ((int64_t)1 << 31);
-    if (bucket) {
-      DdArgs ba = da;
-      ba.parts = parts;
-      ba.part_slices = g2;
-      ba.group = g2;
-      // the row order reuses the cursor array: kBkClasses + R / 2 <= R + 1
-      ba.rows_per_pass = 1024;
-      static_assert(kBkClasses + 1024 / 2 <= 1024 + 1, "row order does not fit the cursor array");
-      ba.entries_per_pass = (int)ne_all;
-      const size_t blds = 2 * (size_t)(ba.rows_per_pass + 1) * sizeof(int) +
-                          ((size_t)ne_all + (size_t)num_queries) * sizeof(int);
-      if (blds <= max_lds_per_block()) {
-        MAXSIM_DISPATCH(dtype, launch_dd_bucket, ba, blds, out16, st);
-        return check_launch("dd_bucket_kernel");
-      }
-    }
+  if (bucket) {
+    MAXSIM_DISPATCH(dtype, launch_dd_bucket, ba, blds, out16, st);
+    return check_launch("dd_bucket_kernel");
   }
   MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, out16, st);
   return check_launch("dd_contrastive_kernel");
