@@ -14,7 +14,11 @@ user-level step time (including the API's offset validation).
 configurations (C2 contrastive 64x64, C3 padded rerank docs/s, C4 packed
 pairs) and the CPU baseline are extra fields.
 
-    python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
+Before the W warmup steps, untimed C5 training steps run for --settle-ms
+(default 500 ms), since the GPU clock ramps up over the first few hundred ms
+of sustained load; the K timed steps are then full steps at the steady clock.
+
+    python bench.py [--steps K] [--warmup W] [--settle-ms MS] [--quick] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -48,6 +52,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-ms", type=float, default=500.0,
+                   help="untimed C5 training steps for this long before the warmup steps: the "
+                        "GPU clock ramps up over the first few hundred ms of sustained load")
     p.add_argument("--quick", action="store_true", help="headline workload only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--profile-ops", action="store_true",
@@ -564,7 +571,17 @@ def main():
         loss.backward()
         return loss
 
-    log(f"C5: warmup {W} steps (T_d={total})")
+    # Settle: the clock ramps up over the first few hundred ms of sustained
+    # load (one box: the C5 forward at 1.05 ms 30 ms into a run, 0.99 ms at
+    # 360 ms), so untimed training steps run for settle_ms before the W
+    # warmup steps, and the K timed steps see the steady clock.
+    n_settle = 0
+    t_settle = time.perf_counter() + args.settle_ms / 1e3
+    while time.perf_counter() < t_settle:
+        step()
+        n_settle += 1
+    torch.cuda.synchronize()
+    log(f"C5: settle {n_settle} steps ({args.settle_ms:.0f} ms), warmup {W} steps (T_d={total})")
     for _ in range(W):
         step()
     torch.cuda.synchronize()
@@ -604,6 +621,7 @@ def main():
     fwd_tflops = flops_fwd / (ms_fwd * 1e-3) / 1e12
     extra["c5"] = {
         "T_d": total, "flops_fwd": flops_fwd,
+        "settle_ms": args.settle_ms, "settle_steps": n_settle,
         "step_ms": round(ms_step, 4),
         "fused_ce_step_ms": round(ms_step_fused, 4),
         "fwd_ms": round(ms_fwd, 4), "fwd_tflops": round(fwd_tflops, 2),
