@@ -1051,6 +1051,14 @@ __global__ __launch_bounds__(kDdThreads) void dd_contrastive_kernel(DdArgs a) {
 //     of a round have about the same size (documents of at least
 //     kBkOrderMin entries; below that the sort costs more than it saves).
 // ---------------------------------------------------------------------------
+// (a & 0xffff) * (b & 0xffff) + c in one VALU instruction (the compiler
+// selects an AND and a 24-bit multiply-add for the same expression).
+__device__ __forceinline__ uint32_t mad_u16(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(b), "v"(c));
+  return r;
+}
+
 constexpr int kBkBatch = 8;            // bucket entries gathered per step
 constexpr int kBkMaxEntriesPerThread = 32;
 constexpr int kBkClasses = 256;        // row size classes: ceil(entries / 4), capped
@@ -1062,10 +1070,12 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
   extern __shared__ int lds_i[];
   const int R = a.rows_per_pass;
   const int E = a.entries_per_pass;
-  int* start = lds_i;                 // [R + 1]
+  // The staged score gradients come first, at LDS byte 0, so that an
+  // entry id (row x | (query * 4) << 16) holds its weight's LDS address.
+  float* gst = reinterpret_cast<float*>(lds_i);  // [Nq]
+  int* start = lds_i + a.nq;          // [R + 1]
   int* cursor = start + (R + 1);      // [R + 1]
   int* ids = cursor + (R + 1);        // [E]
-  float* gst = reinterpret_cast<float*>(ids + E);  // [Nq]
 
   const int xcd = blockIdx.x % kXcds;
   const int per_part = kXcds / a.parts;
@@ -1167,12 +1177,13 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
     __syncthreads();
     for (int x = tid; x < nrows; x += kDdThreads) cursor[x] = start[x];
     __syncthreads();
-    // 3. scatter packed entry ids (x | query << 16) from the registers
+    // 3. scatter packed entry ids (x | (query * 4) << 16: x < 2^14 and
+    // query < 2^14, host checks) from the registers
 #pragma unroll
     for (int k = 0; k < kBkMaxEntriesPerThread; ++k) {
       if (jj[k] >= 0 && jj[k] < nrows) {
-        const int x = xt + k * kDdThreads;
-        ids[atomicAdd(&cursor[jj[k]], 1)] = x | ((qt + k * q_step) << 16);
+        const uint32_t x = (uint32_t)(xt + k * kDdThreads);
+        ids[atomicAdd(&cursor[jj[k]], 1)] = (int)(x | ((uint32_t)(qt + k * q_step) << 18));
       }
     }
     __syncthreads();
@@ -1246,8 +1257,8 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
           for (int k = 0; k < KB; ++k) {
             ok[k] = !MASKED || s + k < s1;
             const uint32_t v = (uint32_t)ids[ok[k] ? s + k : s];
-            off[k] = __umul24(v & 0xffffu, row_bytes) + k0b;
-            gx[k] = gst[v >> 16];
+            off[k] = mad_u16(v, row_bytes, k0b);
+            gx[k] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gst) + (v >> 16));
           }
           Frag<T> f[KB][NS];
 #pragma unroll
