@@ -75,6 +75,42 @@ def test_contrastive_backward_with_and_without_workspace(lib, dtype, d_lens):
     assert torch.equal(dq0, dq2)
 
 
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_contrastive_backward_unaligned_dq_takes_the_scalar_reduce(lib, grad_dtype):
+    """With a workspace, dD's workgroups also add dQ's eight partial sums;
+    a dQ pointer that is not 16-byte aligned makes that reduce go element by
+    element instead of by 16-byte groups.  Same bits either way."""
+    fn = lib.maxsim_amd_contrastive_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P,
+                   SZ, P]
+    Nq, Lq, dim = 5, 32, 128
+    d_lens = [40, 3, 77, 12, 64, 9, 128, 31, 50]
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, torch.bfloat16, seed=31)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dscore = torch.randn(Nq, len(d_lens), generator=torch.Generator().manual_seed(4)).to(DEVICE)
+    need = lib.maxsim_amd_contrastive_backward_workspace_size(Nq, Lq, dim)
+    ws = torch.empty(need // 4, device=DEVICE)
+    n = Nq * Lq * dim
+    es = torch.tensor([], dtype=grad_dtype).element_size()
+    outs = []
+    for shift in (0, 1):  # elements: 0 keeps 16-byte alignment, 1 breaks it
+        buf = torch.full((n + 16,), float("nan"), device=DEVICE, dtype=grad_dtype)
+        dd = torch.empty(d.shape[0], dim, device=DEVICE, dtype=grad_dtype)
+        rc = fn(DT[torch.bfloat16], DT[grad_dtype], dscore.data_ptr(), q.data_ptr(), Nq, Lq,
+                d.data_ptr(), d.shape[0], off.data_ptr(), len(d_lens), argmax.data_ptr(), dim,
+                buf.data_ptr() + shift * es, dd.data_ptr(), ws.data_ptr(), need,
+                torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib.maxsim_amd_last_error()
+        torch.cuda.synchronize()
+        outs.append(buf[shift:shift + n].reshape(Nq, Lq, dim).clone())
+        # nothing written outside dQ's n elements
+        assert torch.isnan(buf[:shift].float()).all() and torch.isnan(buf[shift + n:].float()).all()
+    assert torch.equal(outs[0], outs[1])
+    dq_ref, _ = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off), npi(argmax))
+    tol = GRAD_TOL[torch.float32] if grad_dtype == torch.float32 else dict(rtol=1e-2, atol=1e-2)
+    assert_close(outs[0], dq_ref, **tol)
+
+
 def test_contrastive_backward_split_is_reproducible(lib):
     q, d, off = make_contrastive(4, 32, 128, [50] * 16, torch.bfloat16, seed=5)
     _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
