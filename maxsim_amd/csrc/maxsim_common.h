@@ -285,4 +285,16 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32
       : "memory");
 }
 
+// The same load with the non-temporal cache policy (`nt`), for data read
+// exactly once (the padded candidates' rows): its lines are marked for early
+// eviction and leave L2 to the data that is re-read.
+__device__ __forceinline__ void lds_dma16_nt(const void* base, uint32_t off, uint32_t m0) {
+  __asm__ __volatile__(
+      "s_nop 4\n\t"
+      "global_load_lds_dwordx4 %0, %1 nt"
+      :
+      : "v"(off), "s"(base), "{m0}"(__builtin_amdgcn_readfirstlane(m0))
+      : "memory");
+}
+
 }  // namespace maxsim
