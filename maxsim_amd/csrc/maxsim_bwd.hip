@@ -121,6 +121,36 @@ __device__ __forceinline__ void* out_at(void* base, int64_t off) {
   return static_cast<char*>(base) + off * O::bytes;
 }
 
+// Non-temporal 16-byte stores, for output rows that nothing re-reads while
+// the kernel runs: their lines are marked for early eviction and leave L2 to
+// the gathered rows.  A wave's stores should cover whole lines (consecutive
+// lanes, consecutive 16-byte pieces): partial lines written this way cost
+// far more than cached ones.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store16_nt(void* p, u32x4_t v) {
+  __builtin_nontemporal_store(v, static_cast<u32x4_t*>(p));
+}
+
+// 8 gradient elements in the output type O, 16-byte aligned (vec rows), as
+// non-temporal stores.
+template <typename O>
+__device__ __forceinline__ void store8_nt(void* row_v, int k0, const float v[8]) {
+  if constexpr (O::bytes == 4) {
+    float* row = static_cast<float*>(row_v) + k0;
+    store16_nt(row, u32x4_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                            __float_as_uint(v[3])});
+    store16_nt(row + 4, u32x4_t{__float_as_uint(v[4]), __float_as_uint(v[5]),
+                                __float_as_uint(v[6]), __float_as_uint(v[7])});
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (uint32_t)to_out16<O>(v[2 * e]) | ((uint32_t)to_out16<O>(v[2 * e + 1]) << 16);
+    store16_nt(static_cast<uint16_t*>(row_v) + k0, u32x4_t{w[0], w[1], w[2], w[3]});
+  }
+}
+
 // 8 gradient elements in the output type O (F32, BF16 or F16).  With vec the
 // row is 16-byte aligned and holds all 8 (dim % 8 == 0).
 template <typename O>
@@ -2002,13 +2032,27 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
         for (int rr = tid; rr < nrows; rr += kGroupThreads)
           if (start[rr + 1] > start[rr]) cursor[atomicAdd(&n_full, 1)] = rr;
         if (first) {
-          const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-          const float inv_sl = 1.0f / (float)sl_hi;
-          for (int x = tid; x < nrows * sl_hi; x += kGroupThreads) {
-            const int rr = div_small(x, sl_hi, inv_sl);
-            if (start[rr + 1] == start[rr])
-              store8<O>(out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim), (x - rr * sl_hi) * 8, dim,
-                        VEC, zero8);
+          if constexpr (VEC) {
+            // 16-byte pieces, consecutive threads on consecutive pieces
+            // (whole lines per wave store), non-temporal: nothing re-reads
+            // them.  C4 backward 230.7 -> 190.2 us (bf16 gradients).
+            const int upr = dim * O::bytes / 16;  // pieces per row
+            const float inv_upr = 1.0f / (float)upr;
+            for (int x = tid; x < nrows * upr; x += kGroupThreads) {
+              const int rr = div_small(x, upr, inv_upr);
+              if (start[rr + 1] == start[rr])
+                store16_nt(out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim + (x - rr * upr) * (16 / O::bytes)),
+                           u32x4_t{0u, 0u, 0u, 0u});
+            }
+          } else {
+            const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            const float inv_sl = 1.0f / (float)sl_hi;
+            for (int x = tid; x < nrows * sl_hi; x += kGroupThreads) {
+              const int rr = div_small(x, sl_hi, inv_sl);
+              if (start[rr + 1] == start[rr])
+                store8<O>(out_at<O>(a.dd, (ds + r0 + rr) * (int64_t)dim), (x - rr * sl_hi) * 8,
+                          dim, VEC, zero8);
+            }
           }
         }
         __syncthreads();
@@ -2088,7 +2132,12 @@ __global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs 
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int sl = sc + gl + u * G;
-            if (sl < sl_hi) store8<O>(dst, sl * 8, dim, VEC, acc[u]);
+            if (sl < sl_hi) {
+              if constexpr (VEC)
+                store8_nt<O>(dst, sl * 8, acc[u]);
+              else
+                store8<O>(dst, sl * 8, dim, VEC, acc[u]);
+            }
           }
         }
       }
