@@ -143,8 +143,11 @@ int maxsim_amd_packed_backward_typed(
 
 /* maxsim_amd_packed_backward_typed without a workspace argument and without
  * any allocation: the pair grouping lists live in a file-scope device array
- * of the library (16 MiB per device, held until the process ends), so the
- * call allocates nothing and its kernels take that array's address.
+ * of the library (16 MiB per device), so the call allocates nothing and its
+ * kernels take that array's address.  The HIP runtime allocates the array
+ * when it loads the library's code object on a device: every process that
+ * loads the library holds 16 MiB on each device it uses, until it ends,
+ * whether or not it calls this entry point.
  * No counterpart in the reference.  It is for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  Limit: 2 * num_queries +

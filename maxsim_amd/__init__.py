@@ -748,24 +748,36 @@ def pack_documents(doc_emb, doc_lengths):
 # ---------------------------------------------------------------------------
 # Contrastive (all pairs)
 # ---------------------------------------------------------------------------
+def _check_targets(t: np.ndarray, nb: int) -> None:
+    bad = np.flatnonzero((t < 0) | (t >= nb))
+    if bad.size:
+        i = int(bad[0])
+        raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {nb})")
+
+
 @torch.compiler.disable
-def _checked_contrastive(queries, documents, document_offsets, launch):
+def _checked_contrastive(queries, documents, document_offsets, launch, targets=None):
     """Validate a contrastive call and return ``launch()``.
 
-    The offsets travel to pinned host memory by an asynchronous copy queued
-    ahead of the kernels, and ``launch()`` queues the kernels before the host
-    waits for that copy, so the GPU is never idle while the host checks them.
-    Invalid offsets raise the same errors as before; the kernels already
-    queued are safe with any offsets (documents with an invalid range give
-    NaN, nothing is read out of range) and their results are dropped."""
+    The offsets (and the cross-entropy targets, when given) travel to pinned
+    host memory by asynchronous copies queued ahead of the kernels, and
+    ``launch()`` queues the kernels before the host waits for those copies,
+    so the GPU is never idle while the host checks them.  Invalid offsets or
+    targets raise the same errors as before; the kernels already queued are
+    safe with any offsets and targets (documents with an invalid range give
+    NaN, a target outside ``[0, Nb)`` a NaN loss, nothing is read out of
+    range) and their results are dropped."""
     _check_contrastive(queries, documents, document_offsets)
     flat = document_offsets.detach().reshape(-1)
+    nb = flat.numel() - 1
     if not _HOST_CHECKS and flat.is_cuda:
         if documents.shape[0] == 0:
             raise ValueError("documents must not be empty (document_offsets has >= 1 document)")
         return launch()
     if not flat.is_cuda:  # host tensors: check first (the operators reject them anyway)
         _check_offsets(flat.numpy().astype(np.int64), documents.shape[0])
+        if targets is not None:
+            _check_targets(_to_host(targets)[0], nb)
         return launch()
     # The copy stays on the current stream: a small copy runs as a blit
     # kernel, and on a side stream it would wait for a free CU until the
@@ -774,11 +786,18 @@ def _checked_contrastive(queries, documents, document_offsets, launch):
     # microseconds between the previous step's work and the forward.
     host = torch.empty(flat.shape, dtype=flat.dtype, pin_memory=True)
     host.copy_(flat, non_blocking=True)
+    host_t = None
+    if targets is not None:
+        tflat = targets.detach().reshape(-1)
+        host_t = torch.empty(tflat.shape, dtype=tflat.dtype, pin_memory=True)
+        host_t.copy_(tflat, non_blocking=True)
     copied = torch.cuda.Event()
     copied.record()
     result = launch()
     copied.synchronize()
     _check_offsets(host.numpy().astype(np.int64), documents.shape[0])
+    if host_t is not None:
+        _check_targets(host_t.numpy().astype(np.int64), nb)
     return result
 
 
@@ -853,7 +872,7 @@ class _ContrastiveCEFn(torch.autograd.Function):
         q, d = queries.contiguous(), documents.contiguous()
         offs = document_offsets.to(torch.int32).contiguous()
         scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, offs)
-        tgt = None if targets is None else targets.to(torch.int32).contiguous()
+        tgt = _targets_i32(targets, offs.numel() - 1)
         lse, loss = ops.maxsim_cross_entropy_forward(scores, tgt, inv_t, reduction)
         if tgt is None:
             ctx.save_for_backward(q, d, offs, argmax, scores, lse)
@@ -895,13 +914,22 @@ def _check_cross_entropy(queries, documents, document_offsets, targets, temperat
         if targets.dim() != 1 or targets.shape[0] != Nq:
             raise ValueError(f"targets must have shape [Nq={Nq}]; got {tuple(targets.shape)}")
         _require_one_device(queries=queries, targets=targets)
-        if _HOST_CHECKS or not targets.is_cuda:
-            t = _to_host(targets)[0]
-            bad = np.flatnonzero((t < 0) | (t >= Nb))
-            if bad.size:
-                i = int(bad[0])
-                raise ValueError(f"targets[{i}] = {int(t[i])} out of range [0, {Nb})")
+        # the values are checked by _checked_contrastive, overlapped with
+        # the kernels (host checks on) or by the kernels (NaN loss, off)
     return 1.0 / temperature, _REDUCTIONS[reduction]
+
+
+def _targets_i32(targets, nb: int):
+    """int32 targets for the kernels.  int64 values outside ``[0, Nb)`` become
+    -1 on the device before the narrowing, so that with host checks off a
+    value such as 2**32 + 1 gives the documented NaN loss instead of wrapping
+    to a valid class (no host wait: capturable)."""
+    if targets is None:
+        return None
+    if targets.dtype == torch.int64:
+        targets = torch.where((targets >= 0) & (targets < nb), targets,
+                              torch.full_like(targets, -1))
+    return targets.to(torch.int32).contiguous()
 
 
 def score_contrastive_cross_entropy(queries, documents, document_offsets, targets=None, *,
@@ -929,7 +957,8 @@ def score_contrastive_cross_entropy(queries, documents, document_offsets, target
                                       temperature, reduction)
     return _checked_contrastive(
         queries, documents, document_offsets,
-        lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets, inv_t, red))
+        lambda: _ContrastiveCEFn.apply(queries, documents, document_offsets, targets, inv_t, red),
+        targets=targets)
 
 
 def score_contrastive_cross_entropy_value_and_grad(queries, documents, document_offsets,
@@ -973,7 +1002,7 @@ def score_contrastive_cross_entropy_value_and_grad(queries, documents, document_
         q, d = queries.detach().contiguous(), documents.detach().contiguous()
         offs = document_offsets.to(torch.int32).contiguous()
         scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, offs)
-        tgt = None if targets is None else targets.to(torch.int32).contiguous()
+        tgt = _targets_i32(targets, offs.numel() - 1)
         lse, loss = ops.maxsim_cross_entropy_forward(scores, tgt, inv_t, red)
         g = grad_loss
         if g is None:
@@ -984,4 +1013,5 @@ def score_contrastive_cross_entropy_value_and_grad(queries, documents, document_
         return loss, dq, dd
 
     with torch.no_grad():
-        return _checked_contrastive(queries, documents, document_offsets, launch)
+        return _checked_contrastive(queries, documents, document_offsets, launch,
+                                    targets=targets)

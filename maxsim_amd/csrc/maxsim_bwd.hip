@@ -1144,7 +1144,9 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
   const int sl_hi = min(sl_lo + a.part_slices, a.nslices);
   const int ne = (int)(a.nq * a.lq);   // every entry in one pass (host checks)
   const int32_t* am_b = a.argmax + b * a.lq;
-  const int am_qstride = (int)(a.nb * a.lq);  // argmax below 2^31 entries (host checks)
+  // The argmax is below 2^31 bytes (host checks), so the 32-bit byte
+  // offsets below cannot wrap.
+  const int am_qstride = (int)(a.nb * a.lq);
   const MAXSIM_GLOBAL char* Qb = uniform_gptr(static_cast<const char*>(a.q));
   const uint32_t row_bytes = (uint32_t)a.dim * (uint32_t)sizeof(S);
   // this lane's NS consecutive slices of a row, from sc (the host makes a
@@ -2389,68 +2391,56 @@ static size_t max_lds_per_block() {
 }
 
 template <typename T, bool VEC, int NS, typename O>
-static void launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st) {
+static int launch_dd_contrastive_v(const DdArgs& a, size_t lds, hipStream_t st) {
   const auto kern = dd_contrastive_kernel<T, VEC, NS, O>;
   if (lds > 64 * 1024) {
     // once per device and instantiation: allow up to the device's maximum
-    static bool raised[64] = {false};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !raised[dev]) {
-      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)max_lds_per_block());
-      (void)hipGetLastError();
-      if (dev >= 0 && dev < 64) raised[dev] = true;
-    }
+    static std::atomic<bool> raised[kMaxDevices];
+    if (int e = raise_lds_limit((const void*)kern, max_lds_per_block(), "dd_contrastive_kernel",
+                                raised))
+      return e;
   }
   const int64_t per_part = kXcds / a.parts;
   const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
+  return MAXSIM_OK;
 }
 
 template <typename T, typename O>
-static void launch_dd_bucket_o(const DdArgs& a, size_t lds, hipStream_t st) {
+static int launch_dd_bucket_o(const DdArgs& a, size_t lds, hipStream_t st) {
   const auto kern = dd_bucket_kernel<T, 1, O>;
   if (lds > 64 * 1024) {
-    static bool raised[64] = {false};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !raised[dev]) {
-      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)max_lds_per_block());
-      (void)hipGetLastError();
-      if (dev >= 0 && dev < 64) raised[dev] = true;
-    }
+    static std::atomic<bool> raised[kMaxDevices];
+    if (int e = raise_lds_limit((const void*)kern, max_lds_per_block(), "dd_bucket_kernel",
+                                raised))
+      return e;
   }
   const int64_t per_part = kXcds / a.parts;
   const int64_t blocks = (a.nb + per_part - 1) / per_part * kXcds;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(kDdThreads), lds, st, a);
+  return MAXSIM_OK;
 }
 
 template <typename T>
-static void launch_dd_bucket(const DdArgs& a, size_t lds, bool out16, hipStream_t st) {
-  if (out16)
-    launch_dd_bucket_o<T, T>(a, lds, st);
-  else
-    launch_dd_bucket_o<T, F32>(a, lds, st);
+static int launch_dd_bucket(const DdArgs& a, size_t lds, bool out16, hipStream_t st) {
+  return out16 ? launch_dd_bucket_o<T, T>(a, lds, st) : launch_dd_bucket_o<T, F32>(a, lds, st);
 }
 
 template <typename T, typename O>
-static void launch_dd_contrastive_o(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
+static int launch_dd_contrastive_o(const DdArgs& a, bool vec, size_t lds, hipStream_t st) {
   const bool two = a.part_slices > a.group;
   if (vec)
-    two ? launch_dd_contrastive_v<T, true, 2, O>(a, lds, st)
-        : launch_dd_contrastive_v<T, true, 1, O>(a, lds, st);
-  else
-    two ? launch_dd_contrastive_v<T, false, 2, O>(a, lds, st)
-        : launch_dd_contrastive_v<T, false, 1, O>(a, lds, st);
+    return two ? launch_dd_contrastive_v<T, true, 2, O>(a, lds, st)
+               : launch_dd_contrastive_v<T, true, 1, O>(a, lds, st);
+  return two ? launch_dd_contrastive_v<T, false, 2, O>(a, lds, st)
+             : launch_dd_contrastive_v<T, false, 1, O>(a, lds, st);
 }
 
 template <typename T>
-static void launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, bool out16,
-                                  hipStream_t st) {
-  if (out16)
-    launch_dd_contrastive_o<T, T>(a, vec, lds, st);
-  else
-    launch_dd_contrastive_o<T, F32>(a, vec, lds, st);
+static int launch_dd_contrastive(const DdArgs& a, bool vec, size_t lds, bool out16,
+                                 hipStream_t st) {
+  return out16 ? launch_dd_contrastive_o<T, T>(a, vec, lds, st)
+               : launch_dd_contrastive_o<T, F32>(a, vec, lds, st);
 }
 
 template <typename T>
@@ -2805,7 +2795,7 @@ static int contrastive_backward_impl(
     if (vec && kDdThreads % Lq == 0 && g2 >= 1 && g2 <= kDdMaxGroup && (g2 & (g2 - 1)) == 0 &&
         g2 * parts == nslices && ne_all <= (int64_t)kDdThreads * kBkMaxEntriesPerThread &&
         q_bytes < ((int64_t)1 << 31) &&
-        num_queries * num_documents * Lq < ((int64_t)1 << 31)) {
+        num_queries * num_documents * Lq * (int64_t)sizeof(int32_t) < ((int64_t)1 << 31)) {
       ba.parts = parts;
       ba.part_slices = g2;
       ba.group = g2;
@@ -2866,10 +2856,16 @@ static int contrastive_backward_impl(
   }
 
   if (bucket) {
-    MAXSIM_DISPATCH(dtype, launch_dd_bucket, ba, blds, out16, st);
+    const int rc = dtype == MAXSIM_BFLOAT16 ? launch_dd_bucket<BF16>(ba, blds, out16, st)
+                   : dtype == MAXSIM_FLOAT16 ? launch_dd_bucket<F16>(ba, blds, out16, st)
+                                             : launch_dd_bucket<F32>(ba, blds, out16, st);
+    if (rc) return rc;
     return check_launch("dd_bucket_kernel");
   }
-  MAXSIM_DISPATCH(dtype, launch_dd_contrastive, da, vec, lds, out16, st);
+  const int rc = dtype == MAXSIM_BFLOAT16 ? launch_dd_contrastive<BF16>(da, vec, lds, out16, st)
+                 : dtype == MAXSIM_FLOAT16 ? launch_dd_contrastive<F16>(da, vec, lds, out16, st)
+                                           : launch_dd_contrastive<F32>(da, vec, lds, out16, st);
+  if (rc) return rc;
   return check_launch("dd_contrastive_kernel");
 }
 

@@ -1083,37 +1083,36 @@ static void launch_wide(const FwdArgs& a, bool vec, hipStream_t st) {
     hipLaunchKernelGGL((wide_pair_kernel<T, false, false>), grid, dim3(256), 0, st, a);
 }
 
-template <typename T, int KS>
-static void launch_ring_ks(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
+template <typename T, int KS, bool ARGMAX, bool STREAM>
+static int launch_ring_v(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
   using G = TileGeom<T, KS>;
   const size_t lds = (size_t)kRingWaves * kRingSlots * G::kBufPieces * sizeof(uint4);
-  auto go = [&](auto kern) {
-    if (lds > 64 * 1024) {
-      // once per device and instantiation: allow the slots' dynamic LDS
-      static bool raised[64] = {false};
-      int dev = 0;
-      if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || !raised[dev]) {
-        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds);
-        (void)hipGetLastError();
-        if (dev >= 0 && dev < 64) raised[dev] = true;
-      }
-    }
-    hipLaunchKernelGGL(kern, grid, dim3(kRingWaves * 64), lds, st, a, ppw);
-  };
+  const auto kern = pair_ring_kernel<T, KS, ARGMAX, STREAM>;
+  if (lds > 64 * 1024) {
+    // once per device and instantiation: allow the slots' dynamic LDS
+    static std::atomic<bool> raised[kMaxDevices];
+    if (int e = raise_lds_limit((const void*)kern, lds, "pair_ring_kernel", raised)) return e;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(kRingWaves * 64), lds, st, a, ppw);
+  return MAXSIM_OK;
+}
+
+template <typename T, int KS>
+static int launch_ring_ks(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
   const bool stream = a.mode == kPadded;
   if (a.argmax)
-    stream ? go(pair_ring_kernel<T, KS, true, true>) : go(pair_ring_kernel<T, KS, true, false>);
-  else
-    stream ? go(pair_ring_kernel<T, KS, false, true>) : go(pair_ring_kernel<T, KS, false, false>);
+    return stream ? launch_ring_v<T, KS, true, true>(a, ppw, grid, st)
+                  : launch_ring_v<T, KS, true, false>(a, ppw, grid, st);
+  return stream ? launch_ring_v<T, KS, false, true>(a, ppw, grid, st)
+                : launch_ring_v<T, KS, false, false>(a, ppw, grid, st);
 }
 
 template <typename T>
-static void launch_ring(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
+static int launch_ring(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
   switch (ks_for_dim(a.dim)) {
-    case 2: launch_ring_ks<T, 2>(a, ppw, grid, st); break;
-    case 4: launch_ring_ks<T, 4>(a, ppw, grid, st); break;
-    default: launch_ring_ks<T, 8>(a, ppw, grid, st); break;
+    case 2: return launch_ring_ks<T, 2>(a, ppw, grid, st);
+    case 4: return launch_ring_ks<T, 4>(a, ppw, grid, st);
+    default: return launch_ring_ks<T, 8>(a, ppw, grid, st);
   }
 }
 
@@ -1145,10 +1144,9 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
     const int ppw_r = a.npairs > 32768 ? 1 : ppw;
     const int64_t waves = (a.npairs + ppw_r - 1) / ppw_r;
     const dim3 grid((unsigned)((waves + kRingWaves - 1) / kRingWaves));
-    switch (dtype) {
-      case MAXSIM_BFLOAT16: launch_ring<BF16>(a, ppw_r, grid, st); break;
-      default: launch_ring<F16>(a, ppw_r, grid, st); break;
-    }
+    const int rc = dtype == MAXSIM_BFLOAT16 ? launch_ring<BF16>(a, ppw_r, grid, st)
+                                            : launch_ring<F16>(a, ppw_r, grid, st);
+    if (rc) return rc;
     return check_launch("pair_ring_kernel");
   }
   switch (dtype) {

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/maxsim_amd.h"
 
 namespace maxsim {
@@ -28,6 +30,32 @@ inline int check_dim(int64_t dim) {
     return fail(MAXSIM_ERR_UNSUPPORTED,
                 "dim %lld exceeds the largest supported embedding dim (%d)",
                 (long long)dim, MAXSIM_AMD_MAX_DIM);
+  return MAXSIM_OK;
+}
+
+// Raise a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per device.  `raised` is the calling kernel instantiation's own per-device
+// flag array; a flag is set only after hipFuncSetAttribute succeeded, so a
+// failure is reported (MAXSIM_ERR_LAUNCH, nothing launched) and tried again
+// on the next call.  Two threads launching at once may both set the
+// attribute, which is idempotent; the flags are atomic.
+constexpr int kMaxDevices = 64;
+inline int raise_lds_limit(const void* kern, size_t bytes, const char* what,
+                           std::atomic<bool> (&raised)[kMaxDevices]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return fail(MAXSIM_ERR_LAUNCH, "%s: no current HIP device", what);
+  }
+  if (dev < kMaxDevices && raised[dev].load(std::memory_order_acquire)) return MAXSIM_OK;
+  const hipError_t e =
+      hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MAXSIM_ERR_LAUNCH, "%s: raising the LDS limit to %zu bytes failed: %s", what,
+                bytes, hipGetErrorString(e));
+  }
+  if (dev < kMaxDevices) raised[dev].store(true, std::memory_order_release);
   return MAXSIM_OK;
 }
 

@@ -97,6 +97,40 @@ def test_cross_entropy_target_out_of_range_is_nan_row(no_checks):
     _same(loss[[0, 2, 3]], ref[[0, 2, 3]])
 
 
+def test_cross_entropy_int64_target_beyond_int32_is_nan_row(no_checks):
+    """An int64 target that would wrap to a valid class when narrowed to
+    int32 (2**32 + 1 -> 1) still gives the NaN loss of an invalid target."""
+    q, d, off = make_contrastive(4, 16, 64, [20, 30, 12, 9, 40], torch.bfloat16, seed=3,
+                                 unit=True)
+    targets = torch.tensor([0, 2**32 + 1, 2, -(2**32) + 3], dtype=torch.int64, device=DEVICE)
+    loss = maxsim_amd.score_contrastive_cross_entropy(q, d, off, targets, reduction="none")
+    torch.cuda.synchronize()
+    assert torch.isnan(loss[1]) and torch.isnan(loss[3])
+    assert torch.isfinite(loss[[0, 2]]).all()
+    vloss, _, _ = maxsim_amd.score_contrastive_cross_entropy_value_and_grad(
+        q, d, off, targets, reduction="none")
+    torch.cuda.synchronize()
+    assert torch.isnan(vloss[1]) and torch.isnan(vloss[3])
+    _same(vloss[[0, 2]], loss[[0, 2]])
+
+
+def test_cross_entropy_device_targets_checked_after_launch():
+    """With host checks on, device targets are copied with the offsets and
+    checked while the kernels run; an out-of-range one still raises."""
+    q, d, off = make_contrastive(4, 16, 64, [20, 30, 12, 9, 40], torch.bfloat16, seed=3,
+                                 unit=True)
+    for bad in (torch.tensor([0, 7, 2, 4], device=DEVICE),
+                torch.tensor([0, 1, -1, 4], dtype=torch.int32, device=DEVICE),
+                torch.tensor([0, 2**32 + 1, 2, 4], device=DEVICE)):
+        with pytest.raises(ValueError, match="out of range"):
+            maxsim_amd.score_contrastive_cross_entropy(q, d, off, bad)
+        with pytest.raises(ValueError, match="out of range"):
+            maxsim_amd.score_contrastive_cross_entropy_value_and_grad(q, d, off, bad)
+    ok = torch.tensor([0, 1, 2, 4], device=DEVICE)
+    loss = maxsim_amd.score_contrastive_cross_entropy(q, d, off, ok, reduction="none")
+    assert torch.isfinite(loss).all()
+
+
 def test_padded_invalid_lengths_nan_only_there(no_checks):
     q, d, ql, dl = make_padded(3, 5, 16, 40, 64, torch.bfloat16, seed=4)
     with maxsim_amd.host_checks(True):

@@ -6,8 +6,9 @@ maxsim_cuda/maxsim.cu:59-126, 647-698).  Here dims up to 256 keep the query
 blocks in registers; wider rows take wide_pair_kernel (operands streamed in
 K-chunks) in the forward and slice-chunk loops in the backward.  The cases
 cover a dim that is not a multiple of 16 (element-wise loads), the dims of
-common embedding models, and one above 2048, where the contrastive dQ takes
-the single-pass gather and the packed dQ covers a row in several rounds."""
+common embedding models, dims above 2048, where the contrastive dQ takes
+the single-pass gather and the packed dQ covers a row in several rounds, and
+the largest accepted dim (16384, MAXSIM_AMD_MAX_DIM: a 64 KiB fp32 row)."""
 
 from __future__ import annotations
 
@@ -25,7 +26,8 @@ from ._helpers import (DEVICE, DTYPES, GRAD_TOL, SCORE_TOL, assert_close, assert
 pytestmark = pytest.mark.gpu
 
 DIMS = [pytest.param(300, id="d300"), pytest.param(384, id="d384"),
-        pytest.param(768, id="d768"), pytest.param(2560, id="d2560")]
+        pytest.param(768, id="d768"), pytest.param(2560, id="d2560"),
+        pytest.param(4096, id="d4096"), pytest.param(16384, id="d16384")]
 _ids = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
 
 
