@@ -2335,6 +2335,12 @@ static bool launch_dq_range(const DqArgs& a, float* ws, bool vec, bool off32, bo
     return false;
   const int rpw = (64 / a.nslices) * kRangeItems;
   const int64_t wgs = (a.rows + 4 * rpw - 1) / (4 * rpw);
+  // Below two workgroups per CU (8192 query rows at dim 128) each workgroup
+  // walks its range with one wave per SIMD and waits on every gather:
+  // dq_split_kernel's smaller workgroups fill the chip instead (same bits).
+  // 64 x 512 documents (one GPU's shard of C5 over 8): 46 -> 21 us; 128
+  // queries: 112 -> 102 us for the whole backward.
+  if (wgs * kXcds < 2 * (int64_t)device_cus()) return false;
   const dim3 grid((unsigned)(wgs * kXcds));
   switch (a.nslices) {
     case 1: hipLaunchKernelGGL((dq_range_kernel<T, 1>), grid, dim3(256), 0, st, a, ws); break;

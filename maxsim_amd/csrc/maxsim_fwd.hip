@@ -1157,19 +1157,6 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
   return check_launch("pair_kernel");
 }
 
-// Compute units of the current device (256 on MI355X), cached per device.
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cached[dev] = v;
-  }
-  return cached[dev];
-}
 
 // Blocks per wave for the tiled kernel, per (dtype width, KS): the query
 // fragments (NBW * KS * {4,8} VGPRs) must leave room for the document

@@ -33,6 +33,27 @@ inline int check_dim(int64_t dim) {
   return MAXSIM_OK;
 }
 
+// Compute units of the current device (256 on MI355X), cached per device
+// (every thread that fills a slot writes the same value).
+inline int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0) {
+      (void)hipGetLastError();
+      v = 256;
+    }
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // Raise a kernel's dynamic-LDS limit to `bytes` on the current device, once
 // per device.  `raised` is the calling kernel instantiation's own per-device
 // flag array; a flag is set only after hipFuncSetAttribute succeeded, so a

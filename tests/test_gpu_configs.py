@@ -223,3 +223,29 @@ def test_c5_backward_in_input_dtype_equals_cast_fp32(c5):
     assert torch.equal(dq, dq32.to(torch.bfloat16))
     _, mag = ops.maxsim_contrastive_backward(g.abs(), q.abs(), d, off, argmax)
     assert_rounded_from(dd, dd32, mag)
+
+
+def test_c5_shard_of_8_forward_and_backward(c5):
+    """One GPU's shard of C5 split by query rows over 8 GPUs: 64 queries
+    against all 512 documents, the per-rank shape of the multi-GPU design
+    (its backward takes the small-batch dQ path).  Forward, fp32 backward and
+    the typed backward against the oracle."""
+    q, d, off, _, _, _ = c5
+    qs = q[:64].contiguous()
+    nb = off.numel() - 1
+    scores, argmax = ops.maxsim_contrastive_forward_with_argmax(qs, d, off)
+    qn, dn, on = np64(qs), np64(d), npi(off)
+    s_ref, a_ref = oracle.contrastive_forward(qn, dn, on)
+    assert_close(scores, s_ref, **SCORE_TOL[torch.bfloat16])
+    check_argmax(npi(argmax), a_ref, lambda idx: qn[idx[0], idx[2]],
+                 lambda idx, j: dn[on[idx[1]] + j])
+    g = ((torch.softmax(scores, 1) - torch.eye(64, nb, device=DEVICE)) / 64).contiguous()
+    dq, dd = ops.maxsim_contrastive_backward(g, qs, d, off, argmax)
+    dq_ref, dd_ref = oracle.contrastive_backward(g.double().cpu().numpy(), qn, dn, on,
+                                                 npi(argmax))
+    assert_close(dq, dq_ref, **GRAD_TOL[torch.bfloat16])
+    assert_close(dd, dd_ref, **GRAD_TOL[torch.bfloat16])
+    dqt, ddt = ops.maxsim_contrastive_backward_typed(g, qs, d, off, argmax)
+    assert torch.equal(dqt, dq.to(torch.bfloat16))
+    _, mag = ops.maxsim_contrastive_backward(g.abs(), qs.abs(), d, off, argmax)
+    assert_rounded_from(ddt, dd, mag)
