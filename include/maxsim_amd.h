@@ -91,6 +91,33 @@ int maxsim_amd_packed_forward_with_argmax(
     const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
     int64_t max_q_len, float* scores, int32_t* argmax, void* stream);
 
+/* Bytes of device workspace that let maxsim_amd_packed_forward_with_argmax_ws
+ * score the pairs document by document: 8 * (ceil(num_pairs / 4) +
+ * min(num_documents, num_pairs)) + 8 + 4 * num_pairs + 4 * (3 * num_documents
+ * + 1).  No counterpart in the reference, whose packed forward scores the
+ * pairs in the caller's order. */
+size_t maxsim_amd_packed_forward_workspace_size(int64_t num_documents, int64_t num_pairs);
+
+/* Replaces ops `maxsim_packed_forward_with_argmax` (torch_binding.h:101-108,
+ * maxsim.cu:2039-2108) and, with argmax NULL, `maxsim_forward`
+ * (torch_binding.h:21-27), like the two entry points above, with a
+ * workspace (device memory, 8-byte aligned, at least
+ * maxsim_amd_packed_forward_workspace_size() bytes): the pairs are grouped by
+ * document on the device and each document's rows are read from memory once
+ * per four of its pairs rather than once per pair.  Taken for 16-bit inputs
+ * of dim 64 or 128 with max_q_len <= 64, at most 16384 documents and at
+ * least 4096 pairs; otherwise, or with a NULL, misaligned or smaller
+ * workspace, this is the entry point without one.  Same results, bit for
+ * bit, either way. */
+int maxsim_amd_packed_forward_with_argmax_ws(
+    maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
+    const int32_t* query_offsets, int64_t num_queries, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* pair_query_ids,
+    const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
+    int64_t max_q_len, float* scores, int32_t* argmax, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* Bytes of device workspace that let maxsim_amd_packed_backward group the
  * pairs by query and by document on the device and compute each gradient
  * row once, without floating-point atomics: 4 * (2 * num_queries + 1 +

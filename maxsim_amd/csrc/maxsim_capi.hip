@@ -33,7 +33,7 @@ int check_launch(const char* what) {
 
 extern "C" {
 
-int maxsim_amd_abi_version(void) { return 9; }
+int maxsim_amd_abi_version(void) { return 10; }
 
 const char* maxsim_amd_last_error(void) { return maxsim::g_error.c_str(); }
 

@@ -1010,6 +1010,571 @@ __global__ __launch_bounds__(kRingWaves * 64) void pair_ring_kernel(FwdArgs a, i
 }
 
 // ---------------------------------------------------------------------------
+// Packed pairs, document-major (doc_chunk_kernel; needs a workspace).
+//
+// Packed pairs come in the caller's order (C4: 20,000 pairs drawn uniformly
+// over 8,192 documents, about 2.4 per document), so scored pair by pair
+// every document is streamed from HBM once per pair that names it, with
+// almost no L2 reuse.  Here the pairs are first grouped by document on the
+// device (group_docs_kernel) and cut into chunks of at most kChunkPairs
+// pairs of one document.  A workgroup of kChunkPairs waves scores a chunk,
+// one pair per wave (the query's one or two 32-token blocks in registers, as
+// in pair_ring_kernel), while the document's tiles pass once through a ring
+// of LDS slots shared by the waves: each wave issues its share of every
+// tile's direct global->LDS loads, waits for them, and one barrier per tile
+// makes the tile visible to all and frees the slot read one tile before.
+// Query blocks travel through the same ring (vector-memory loads complete
+// in issue order, so any other load would make its wait a wait for every
+// tile in flight).  Chunks are sorted by their document's tile count,
+// longest first, and dealt round-robin over a grid that is resident at once,
+// so every workgroup gets a similar share and ends on short chunks.
+// Each pair sees the same MFMA order and tile epilogue as in pair_kernel,
+// so the results are bit-identical whichever kernel scores it.
+// ---------------------------------------------------------------------------
+constexpr int kChunkPairs = 4;                // pairs per chunk (a set of pair waves)
+constexpr int kChunkSets = 1;                 // sets of pair waves, alternating chunks
+constexpr int kChunkLoaders = 1;              // loader waves
+constexpr int kChunkWaves = kChunkLoaders + kChunkSets * kChunkPairs;
+// LDS ring depth, in tiles: at dim 128, 68 KB per workgroup, two per CU
+// (C4 forward 124-131 us; 147-155 at depth 6 and three per CU, 179 at depth
+// 8 and one per CU, 168-192 with two loader waves)
+constexpr int kChunkSlots = 8;
+
+
+constexpr int kChunkBatch = 64;               // chunks per workgroup, at most
+constexpr int kDocGroupThreads = 1024;
+constexpr int kLenClasses = 64;               // sort keys: tile count, clamped
+constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 9 bytes per document
+
+struct DocChunks {
+  int2* chunks;      // [max chunks] (first index into dlist, pair count)
+  int32_t* nchunks;  // [1]
+  int32_t* dlist;    // [npairs] pair ids grouped by document
+  int32_t* dstart;   // [nd + 1] start of each document's run in dlist
+  int32_t* dcur;     // [nd] the runs' cursors
+  int32_t* cpos;     // [nd] each document's first chunk
+};
+
+// Upper bound on the chunks of a grouping: ceil(c / 4) <= c / 4 + 3 / 4 per
+// document with c > 0 pairs, and at most min(nd, npairs) such documents.
+static int64_t doc_chunk_bound(int64_t nd, int64_t npairs) {
+  return (npairs + kChunkPairs - 1) / kChunkPairs + std::min(nd, npairs);
+}
+
+// NaN score and zero argmax row for a pair no chunk carries (one thread).
+__device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p) {
+  a.scores[p] = __builtin_nanf("");
+  if (a.argmax)
+    for (int t = 0; t < a.slots; ++t) a.argmax[p * a.slots + t] = 0;
+}
+
+// group_docs_kernel (one workgroup): pairs per document (LDS counters),
+// each document's length class (LDS bytes), an exclusive scan of the counts
+// into each document's run in dlist, and each document's first chunk by a
+// counting sort over the length classes (LDS cursors).  Its outputs go out
+// in coalesced passes: a single CU writing scattered words is what costs
+// here (about one cache line per clock), so the scattered writes -- the
+// chunk table and the pair ids -- are left to scatter_docs_kernel, which
+// spreads them over the chip.  The ids and offsets are loaded up front, in
+// independent batches: a one-workgroup kernel takes as long as its chain of
+// dependent round trips.  A pair whose document id is out of range is
+// written off here (NaN score, zero argmax row).  Chunk positions within a
+// class follow the atomics; no result depends on them.
+constexpr int kGroupPairBatch = 24;  // pair ids per thread per batch
+constexpr int kGroupDocBatch = 8;    // document extents per thread per batch
+__global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a, DocChunks g) {
+  extern __shared__ int32_t cnt[];            // [nd] counts, then run starts
+  __shared__ int32_t cls[kLenClasses];        // chunks per class, then cursors
+  __shared__ int32_t wtot[kDocGroupThreads / 64];
+  static_assert(kLenClasses == 64, "one class per lane of wave 0");
+  constexpr int UP = kGroupPairBatch, UD = kGroupDocBatch;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nd = (int)a.nd;
+  const int64_t np = a.npairs;
+  int32_t* cpos = cnt + nd;                                // [nd] first chunk
+  uint8_t* kls = reinterpret_cast<uint8_t*>(cpos + nd);    // [nd] length class
+
+  // the first UP pair ids and UD document extents of this thread, loaded
+  // before anything waits on them
+  int32_t di[UP];
+#pragma unroll
+  for (int u = 0; u < UP; ++u) {
+    const int64_t p = tid + (int64_t)u * kDocGroupThreads;
+    di[u] = p < np ? a.dids[p] : 0;
+  }
+  int32_t o_lo[UD], o_hi[UD];
+#pragma unroll
+  for (int u = 0; u < UD; ++u) {
+    const int d = tid + u * kDocGroupThreads;
+    o_lo[u] = d < nd ? a.doff[d] : 0;
+    o_hi[u] = d < nd ? a.doff[d + 1] : 0;
+  }
+  for (int d = tid; d < nd; d += kDocGroupThreads) cnt[d] = 0;
+  if (tid < kLenClasses) cls[tid] = 0;
+  __syncthreads();
+
+  // 1. pairs per document; a batch holding an out-of-range document id
+  //    writes its pairs off in a second, rolled loop (rare)
+  auto count_batch = [&](int64_t p0) __attribute__((always_inline)) {
+    bool bad = false;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      const bool in = p0 + (int64_t)u * kDocGroupThreads < np;
+      if (in && di[u] >= 0 && di[u] < nd)
+        atomicAdd(&cnt[di[u]], 1);
+      else
+        bad |= in;
+    }
+    if (bad) {
+#pragma unroll 1
+      for (int u = 0; u < UP; ++u) {
+        const int64_t p = p0 + (int64_t)u * kDocGroupThreads;
+        if (p >= np) break;
+        const int32_t d = a.dids[p];
+        if (d < 0 || d >= nd) write_unrouted_pair(a, p);
+      }
+    }
+  };
+  count_batch(tid);
+  for (int64_t p0 = tid + (int64_t)UP * kDocGroupThreads; p0 < np;
+       p0 += (int64_t)UP * kDocGroupThreads) {
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      const int64_t p = p0 + (int64_t)u * kDocGroupThreads;
+      di[u] = p < np ? a.dids[p] : 0;
+    }
+    count_batch(p0);
+  }
+  __syncthreads();
+
+  // 2. length class of every document, and the chunks of each class
+  auto classify = [&](int d, int32_t lo_off, int32_t hi_off) __attribute__((always_inline)) {
+    if (d >= nd) return;
+    const int64_t ld = (int64_t)hi_off - lo_off;
+    const int64_t t = ld <= 0 ? 0 : (ld + kTileRows - 1) / kTileRows;
+    const int k = kLenClasses - 1 - (int)(t < kLenClasses - 1 ? t : kLenClasses - 1);
+    kls[d] = (uint8_t)k;
+    const int c = cnt[d];
+    if (c > 0) atomicAdd(&cls[k], (c + kChunkPairs - 1) / kChunkPairs);
+  };
+#pragma unroll
+  for (int u = 0; u < UD; ++u) classify(tid + u * kDocGroupThreads, o_lo[u], o_hi[u]);
+  for (int d0 = tid + UD * kDocGroupThreads; d0 < nd; d0 += UD * kDocGroupThreads) {
+#pragma unroll
+    for (int u = 0; u < UD; ++u) {
+      const int d = d0 + u * kDocGroupThreads;
+      o_lo[u] = d < nd ? a.doff[d] : 0;
+      o_hi[u] = d < nd ? a.doff[d + 1] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < UD; ++u) classify(d0 + u * kDocGroupThreads, o_lo[u], o_hi[u]);
+  }
+
+  // 3. a run of documents per thread: exclusive scan of the pair counts over
+  //    the workgroup; wave 0 also scans the class counts
+  const int per = (nd + kDocGroupThreads - 1) / kDocGroupThreads;
+  const int lo = min(tid * per, nd), hi = min(lo + per, nd);
+  int run = 0;
+  for (int d = lo; d < hi; ++d) run += cnt[d];
+  int incl = run;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < kDocGroupThreads / 64 ? wtot[lane] : 0;
+    const int cc = cls[lane];
+    int ci = cc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(w, off);
+      const int u = __shfl_up(ci, off);
+      if (lane >= off) {
+        w += t;
+        ci += u;
+      }
+    }
+    if (lane < kDocGroupThreads / 64) wtot[lane] = w;  // inclusive over waves
+    cls[lane] = ci - cc;                              // first chunk of the class
+    if (lane == 63) g.nchunks[0] = ci;
+  }
+  __syncthreads();
+
+  // 4. run starts (in place of the counts) and first chunks
+  int start = incl - run + (wave > 0 ? wtot[wave - 1] : 0);
+  for (int d = lo; d < hi; ++d) {
+    const int c = cnt[d];
+    cnt[d] = start;
+    if (c > 0) cpos[d] = atomicAdd(&cls[kls[d]], (c + kChunkPairs - 1) / kChunkPairs);
+    start += c;
+  }
+  __syncthreads();
+
+  // 5. coalesced copy-out: run starts (and the total after the last), the
+  //    scatter's cursors, first chunks
+  for (int d = tid; d < nd; d += kDocGroupThreads) {
+    const int s = cnt[d];
+    g.dstart[d] = s;
+    g.dcur[d] = s;
+    g.cpos[d] = cpos[d];
+  }
+  if (tid == kDocGroupThreads - 1) g.dstart[nd] = wtot[kDocGroupThreads / 64 - 1];
+}
+
+// scatter_docs_kernel (grid-stride, many workgroups): each pair id into its
+// document's run (global cursors), and each document's chunks into the
+// chunk table at its first chunk: (first index in dlist, up to kChunkPairs
+// pairs).  The order inside a run follows the atomics; no result depends
+// on it.
+__global__ __launch_bounds__(256) void scatter_docs_kernel(FwdArgs a, DocChunks g) {
+  const int nd = (int)a.nd;
+  const int64_t np = a.npairs;
+  const int64_t n = np > nd ? np : nd;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    if (i < np) {
+      const int32_t d = a.dids[i];
+      if (d >= 0 && d < nd) g.dlist[atomicAdd(&g.dcur[d], 1)] = (int32_t)i;
+    }
+    if (i < nd) {
+      const int s = g.dstart[i];
+      const int c = g.dstart[i + 1] - s;
+      if (c > 0) {
+        const int base = g.cpos[i];
+        for (int j = 0; j * kChunkPairs < c; ++j)
+          g.chunks[base + j] = make_int2(s + j * kChunkPairs, min(kChunkPairs, c - j * kChunkPairs));
+      }
+    }
+  }
+}
+
+// A chunk as the scoring workgroup sees it, resolved once into LDS before
+// any tile load: the document's rows and, per pair slot, its pair.
+struct ChunkMeta {
+  int d_row0;
+  int ld;                      // 0: the document's segment is invalid
+  int pad[2];
+  int p[kChunkPairs];          // pair id; -1: no pair in this slot
+  int q_row0[kChunkPairs];
+  int lq[kChunkPairs];         // 0: invalid pair (NaN score)
+};
+
+// LDS per workgroup of doc_chunk_kernel (ring + chunk metadata; 68 KB at
+// dim 128: two workgroups per CU), and the waves per SIMD its register
+// budget is compiled for: a workgroup of five waves takes two wave slots on
+// some SIMD, so two workgroups per CU need four slots per SIMD, i.e. at most
+// 128 VGPRs (at 154 VGPRs the runtime places one workgroup per CU: C4
+// forward 175 against 124-131 us).
+template <typename T, int KS>
+struct ChunkOcc {
+  static constexpr int kLds =
+      kChunkSlots * TileGeom<T, KS>::kBufPieces * 16 + kChunkBatch * (int)sizeof(ChunkMeta);
+  static constexpr int kWavesPerEu = 2 * ((kChunkWaves + 3) / 4);
+};
+
+// Chunk of round r for workgroup b of `grid`: the sorted chunks are dealt
+// in snake order (b, then grid - 1 - b, ...) so that no workgroup takes the
+// largest chunk of every round.
+__device__ __forceinline__ int64_t snake_chunk(int b, int r, int grid) {
+  return (int64_t)r * grid + ((r & 1) ? grid - 1 - b : b);
+}
+
+// s_waitcnt vmcnt(N) (N <= 63); encoding (gfx9): vmcnt[3:0] | expcnt[6:4]
+// = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// The workgroup: kChunkLoaders loader waves and kChunkSets sets of
+// kChunkPairs pair waves.  The loaders issue every global->LDS tile load of
+// the ring (each its share of every tile) and nothing else, so their
+// vector-memory counters see only the ring and their waits are exact.  Set
+// s scores the chunks c with c % kChunkSets == s, wave j of the set pair
+// slot j; it loads the query blocks of its next chunk straight into
+// registers with ordinary loads (counted by the compiler, behind no tile
+// load) as soon as it has finished a chunk, so they arrive while the other
+// set scores.  One barrier per tile: the loaders have waited for the tile's
+// loads, every pair wave has finished reading the slot of the tile before,
+// and the loaders refill that slot.
+template <typename T, int KS, bool ARGMAX, bool STREAM>
+__global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) void doc_chunk_kernel(
+    FwdArgs a, const int2* __restrict__ chunks, const int32_t* __restrict__ nchunks_p,
+    const int32_t* __restrict__ dlist) {
+  using S = typename T::storage;
+  using G = TileGeom<T, KS>;
+  static_assert(T::bytes == 2, "16-bit operands: one 16-byte piece per fragment");
+  constexpr int QB = 2;
+  constexpr int kRPI = 64 / G::P;                 // tile rows per wave load instruction
+  constexpr int kDma = G::kPieces / 64;           // wave load instructions per tile
+  constexpr int kDmaL = kDma / kChunkLoaders;     // ... issued by each loader
+  static_assert(kDma % kChunkLoaders == 0 && kDmaL >= 1, "tile loads split evenly");
+  static_assert(kDmaL * (kChunkSlots - 1) <= 63, "a loader's tiles in flight fit vmcnt");
+  extern __shared__ uint4 lds[];
+  ChunkMeta* meta = reinterpret_cast<ChunkMeta*>(lds + kChunkSlots * G::kBufPieces);
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nch = __builtin_amdgcn_readfirstlane(nchunks_p[0]);
+  const int b = blockIdx.x;
+  const int grid = gridDim.x;
+  // chunks of this workgroup: every full round, plus the last round's if it
+  // falls inside; the host sizes the grid so that there are at most
+  // kChunkBatch rounds
+  const int rounds = nch / grid;
+  const int mine =
+      min(rounds + (snake_chunk(b, rounds, grid) < nch ? 1 : 0), kChunkBatch);
+  if (mine == 0) return;  // whole workgroup
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(S);
+
+  // ---- chunk metadata: thread s resolves pair slot s % 4 of chunk s / 4;
+  // every index read from device memory is range-checked
+  for (int s = threadIdx.x; s < mine * kChunkPairs; s += kChunkWaves * 64) {
+    const int ci = s / kChunkPairs, j = s - ci * kChunkPairs;
+    const int2 ch = chunks[snake_chunk(b, ci, grid)];
+    int p = -1, q0 = 0, lq = 0, d0 = 0, ld = 0;
+    if (j < ch.y && ch.x + j >= 0 && ch.x + j < a.npairs) {
+      p = dlist[ch.x + j];
+      if (p < 0 || p >= a.npairs) p = -1;
+    }
+    if (p >= 0) {
+      const int64_t qi = a.qids[p], di = a.dids[p];
+      if (di >= 0 && di < a.nd) {
+        const int64_t ds = a.doff[di], de = a.doff[di + 1];
+        if (ds >= 0 && de > ds && de <= a.total_d) {
+          d0 = (int)ds;
+          ld = (int)(de - ds);
+          if (qi >= 0 && qi < a.nq) {
+            const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
+            if (qs >= 0 && qe > qs && qe <= a.total_q && qe - qs <= a.slots) {
+              q0 = (int)qs;
+              lq = (int)(qe - qs);
+            }
+          }
+        }
+      }
+    }
+    ChunkMeta& m = meta[ci];
+    m.p[j] = p;
+    m.q_row0[j] = q0;
+    m.lq[j] = lq;
+    if (j == 0) {
+      m.d_row0 = d0;
+      m.ld = ld;
+    }
+  }
+  __syncthreads();
+
+  // tiles of chunk ci (wave-uniform): none when no pair of it is valid
+  auto chunk_tiles = [&](int ci) __attribute__((always_inline)) {
+    const ChunkMeta& m = meta[ci];
+    int any = 0;
+#pragma unroll
+    for (int j = 0; j < kChunkPairs; ++j) any |= __builtin_amdgcn_readfirstlane(m.lq[j]);
+    return any > 0 ? (__builtin_amdgcn_readfirstlane(m.ld) + kTileRows - 1) / kTileRows : 0;
+  };
+  // s_barrier without a fence (a fence would wait for every load in
+  // flight); the empty asm statements keep the compiler from moving memory
+  // accesses across it
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+  };
+
+  if (wv < kChunkLoaders) {
+    // ---- loader waves: the tile stream, kChunkSlots - 1 tiles ahead
+    const int l_hi = lane / G::P;
+    const int l_lo = lane - l_hi * G::P;
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    int li = 0, lt = 0;  // chunk and tile of the next load
+    int lnt = chunk_tiles(0);
+    while (lnt == 0 && ++li < mine) lnt = chunk_tiles(li);
+    int issued = 0, lslot = 0;
+    auto load_next = [&]() __attribute__((always_inline)) {
+      if (li >= mine) return;
+      const int d0 = __builtin_amdgcn_readfirstlane(meta[li].d_row0);
+      const int ld = __builtin_amdgcn_readfirstlane(meta[li].ld);
+      const S* base = D + ((int64_t)d0 + (int64_t)lt * kTileRows) * dim;
+      const int last = ld - 1 - lt * kTileRows;
+#pragma unroll
+      for (int ii = 0; ii < kDmaL; ++ii) {
+        const int i = wv * kDmaL + ii;
+        const int r = i * kRPI + l_hi;
+        const uint32_t off = (uint32_t)min(r, last) * row_bytes +
+                             (uint32_t)((l_lo ^ (r & G::SWZ)) * 16);
+        const uint32_t dst =
+            ring_lds + (uint32_t)((lslot * G::kBufPieces + i * 64) * sizeof(uint4));
+        if (STREAM)
+          lds_dma16_nt(base, off, dst);
+        else
+          lds_dma16(base, off, dst);
+      }
+      ++issued;
+      if (++lslot == kChunkSlots) lslot = 0;
+      if (++lt >= lnt) {
+        lt = 0;
+        while (++li < mine && (lnt = chunk_tiles(li)) == 0) {
+        }
+      }
+    };
+    // wait until this loader's loads of the tile `ahead` tiles before the
+    // newest issued one have landed
+    auto wait_tile = [&](int ahead) __attribute__((always_inline)) {
+      static_assert(kChunkSlots - 2 <= 14, "wait_tile covers up to 14 tiles ahead");
+      switch (ahead) {
+        case 1: wait_vmcnt<kDmaL * 1>(); break;
+        case 2: wait_vmcnt<kDmaL * 2>(); break;
+        case 3: wait_vmcnt<kDmaL * 3>(); break;
+        case 4: wait_vmcnt<kDmaL * 4>(); break;
+        case 5: wait_vmcnt<kDmaL * 5>(); break;
+        case 6: wait_vmcnt<kDmaL * 6>(); break;
+        case 7: wait_vmcnt<kDmaL * 7>(); break;
+        case 8: wait_vmcnt<kDmaL * 8 <= 63 ? kDmaL * 8 : 0>(); break;
+        case 9: wait_vmcnt<kDmaL * 9 <= 63 ? kDmaL * 9 : 0>(); break;
+        case 10: wait_vmcnt<kDmaL * 10 <= 63 ? kDmaL * 10 : 0>(); break;
+        case 11: wait_vmcnt<kDmaL * 11 <= 63 ? kDmaL * 11 : 0>(); break;
+        case 12: wait_vmcnt<kDmaL * 12 <= 63 ? kDmaL * 12 : 0>(); break;
+        case 13: wait_vmcnt<kDmaL * 13 <= 63 ? kDmaL * 13 : 0>(); break;
+        case 14: wait_vmcnt<kDmaL * 14 <= 63 ? kDmaL * 14 : 0>(); break;
+        default: wait_vmcnt<0>(); break;
+      }
+    };
+    for (int i = 0; i < kChunkSlots - 1; ++i) load_next();
+    int k = 0;
+    for (int ci = 0; ci < mine; ++ci) {
+      const int nt = chunk_tiles(ci);
+      for (int t = 0; t < nt; ++t, ++k) {
+        wait_tile(issued - k - 1);
+        barrier();
+        load_next();  // into the slot of tile k - 1, which no wave reads any more
+      }
+    }
+    // drain: no load may still be writing LDS when the wave exits
+    wait_vmcnt<0>();
+    return;
+  }
+
+  // ---- pair waves
+  const int pw = wv - kChunkLoaders;
+  const int set = pw / kChunkPairs;
+  const int j = pw - set * kChunkPairs;  // pair slot
+  int aoff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) aoff[s] = c * G::P + ((2 * s + h) ^ (c & G::SWZ));
+  Frag<T> qf[QB][KS];
+  // query blocks of this wave's pair in chunk ci into registers: lane (c, h)
+  // takes pieces 2s + h of token c (rows past the query end repeat its last
+  // token) -- the fragments a tile read of the same rows gives
+  auto load_query = [&](int ci) __attribute__((always_inline)) {
+    const int mq = __builtin_amdgcn_readfirstlane(meta[ci].lq[j]);
+    const int q0 = __builtin_amdgcn_readfirstlane(meta[ci].q_row0[j]);
+    const int nblk = (mq + kTileCols - 1) / kTileCols;  // <= QB (host checks)
+    const auto* qg = uniform_gptr(reinterpret_cast<const char*>(Q + (int64_t)q0 * dim));
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (qb < nblk) {
+        const uint32_t row = qb * kTileCols + min(c, mq - 1 - qb * kTileCols);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          qf[qb][s].v = load16(qg, (row * (uint32_t)dim + (2 * s + h) * G::kPieceElems) *
+                                       (uint32_t)sizeof(S));
+      }
+    }
+  };
+  if (set < mine) load_query(set);
+  int cslot = 0;  // slot of the next tile
+  for (int ci = 0; ci < mine; ++ci) {
+    const int nt = chunk_tiles(ci);
+    if (ci % kChunkSets != set) {
+      // the other set's chunk: keep the barriers
+      for (int t = 0; t < nt; ++t) {
+        barrier();
+        if (++cslot == kChunkSlots) cslot = 0;
+      }
+      continue;
+    }
+    const int p = __builtin_amdgcn_readfirstlane(meta[ci].p[j]);
+    const int mq = __builtin_amdgcn_readfirstlane(meta[ci].lq[j]);
+    const int nblk = (mq + kTileCols - 1) / kTileCols;
+    if (p >= 0 && nblk == 0) write_invalid_pair(a, p, lane);
+    float m[QB];
+    int am[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      m[qb] = -__builtin_inff();
+      am[qb] = 0;
+    }
+    auto walk = [&](auto na_const) __attribute__((always_inline)) {
+      constexpr int NA = decltype(na_const)::value;
+      auto tile_step = [&](int t) __attribute__((always_inline)) {
+        // this wave's reads of the previous tile have returned
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        barrier();
+        if constexpr (NA > 0) {
+          const uint4* tile = lds + cslot * G::kBufPieces;
+          Frag<T> df[KS];
+#pragma unroll
+          for (int s = 0; s < KS; ++s) df[s].v = tile[aoff[s]];
+          f32x16 acc[NA];
+#pragma unroll
+          for (int qb = 0; qb < NA; ++qb) {
+            acc[qb] = f32x16{};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[qb][s], acc[qb]);
+          }
+#pragma unroll
+          for (int qb = 0; qb < NA; ++qb)
+            tile_update<ARGMAX>(acc[qb], m[qb], am[qb], t * kTileRows + 4 * h);
+        }
+        if (++cslot == kChunkSlots) cslot = 0;
+      };
+      // The first tile apart: the compiler's waits for the query loads land
+      // in it, and the loop over the rest carries none (a wait left in the
+      // loop would also wait, every tile, for the stores issued since).
+      if (nt > 0) tile_step(0);
+      for (int t = 1; t < nt; ++t) tile_step(t);
+    };
+    if (nblk == 1)
+      walk(std::integral_constant<int, 1>{});
+    else if (nblk == 2)
+      walk(std::integral_constant<int, QB>{});
+    else
+      walk(std::integral_constant<int, 0>{});
+    // this set's next chunk: its query loads go out before this chunk's
+    // score and argmax stores, so that the wait for them (vector-memory
+    // operations complete in order) does not also wait for the stores
+    if (ci + kChunkSets < mine) load_query(ci + kChunkSets);
+    if (nblk > 0) {
+      float score = 0.0f;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        if (qb < nblk) {
+          merge_halves(m[qb], am[qb]);
+          const int tok = qb * kTileCols + c;
+          const bool valid = tok < mq;
+          score += half_sum(valid ? m[qb] : 0.0f);
+          if (ARGMAX && h == 0 && tok < a.slots)
+            a.argmax[(int64_t)p * a.slots + tok] = valid ? am[qb] : 0;
+        }
+      }
+      if (ARGMAX) {
+        for (int t = nblk * kTileCols + lane; t < a.slots; t += 64)
+          a.argmax[(int64_t)p * a.slots + t] = 0;
+      }
+      if (lane == kHalfSumLane) a.scores[p] = score;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side dispatch
 // ---------------------------------------------------------------------------
 static int ks_for_dim(int dim) {
@@ -1114,6 +1679,91 @@ static int launch_ring(const FwdArgs& a, int ppw, dim3 grid, hipStream_t st) {
     case 4: return launch_ring_ks<T, 4>(a, ppw, grid, st);
     default: return launch_ring_ks<T, 8>(a, ppw, grid, st);
   }
+}
+
+// Document-major packed path (doc_chunk_kernel): 16-bit rows of 64 or 128
+// elements (four or eight wave loads per tile, split evenly over the four
+// waves), queries of at most two 32-token blocks, at most kDocGroupMaxDocs
+// documents (one LDS counter each in group_docs_kernel), and enough pairs
+// that the grouping launch pays for itself.
+constexpr int64_t kDocChunkMinPairs = 4096;
+constexpr bool kChunkStream = true;  // document tiles read once: non-temporal
+
+static bool doc_chunk_fits(const FwdArgs& a, maxsim_dtype dtype, int max_lq) {
+  const int ks = ks_for_dim(a.dim);
+  return a.mode == kPacked && dtype != MAXSIM_FLOAT32 && (ks == 4 || ks == 8) &&
+         a.dim == ks * kChunk && aligned16(a.q) && aligned16(a.d) &&
+         max_lq <= 2 * kTileCols && a.nd <= kDocGroupMaxDocs &&
+         a.npairs >= kDocChunkMinPairs && a.npairs <= INT32_MAX;
+}
+
+// Workspace: chunks (int2) [doc_chunk_bound], nchunks (int32, padded to 8
+// bytes), then int32 dlist [npairs], dstart [nd + 1], dcur [nd], cpos [nd].
+static size_t doc_chunk_ws_bytes(int64_t nd, int64_t npairs) {
+  return 8 * (size_t)doc_chunk_bound(nd, npairs) + 8 + 4 * (size_t)npairs + 4 * (3 * (size_t)nd + 1);
+}
+
+// Grid: as many workgroups as the chip holds at once (LDS or registers
+// bound it: three per CU at dim 128), so the chunks are dealt in one round;
+// more only where one workgroup would otherwise get over kChunkBatch.
+template <typename T, int KS, bool ARGMAX>
+static int launch_doc_chunk_v(const FwdArgs& a, const DocChunks& g, int64_t bound,
+                              hipStream_t st) {
+  using G = TileGeom<T, KS>;
+  const size_t lds = ChunkOcc<T, KS>::kLds;
+  const auto kern = doc_chunk_kernel<T, KS, ARGMAX, kChunkStream>;
+  if (lds > 64 * 1024) {
+    static std::atomic<bool> raised[kMaxDevices];
+    if (int e = raise_lds_limit((const void*)kern, lds, "doc_chunk_kernel", raised)) return e;
+  }
+  static std::atomic<int> per_cu[kMaxDevices];
+  const int64_t resident =
+      (int64_t)device_cus() * resident_per_cu((const void*)kern, kChunkWaves * 64, lds, per_cu);
+  const int64_t grid = std::max<int64_t>(resident, (bound + kChunkBatch - 1) / kChunkBatch);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kChunkWaves * 64), lds, st, a,
+                     static_cast<const int2*>(g.chunks), static_cast<const int32_t*>(g.nchunks),
+                     static_cast<const int32_t*>(g.dlist));
+  return MAXSIM_OK;
+}
+
+template <typename T>
+static int launch_doc_chunk(const FwdArgs& a, const DocChunks& g, int64_t bound,
+                            hipStream_t st) {
+  const bool am = a.argmax != nullptr;
+  if (ks_for_dim(a.dim) == 8)
+    return am ? launch_doc_chunk_v<T, 8, true>(a, g, bound, st)
+              : launch_doc_chunk_v<T, 8, false>(a, g, bound, st);
+  return am ? launch_doc_chunk_v<T, 4, true>(a, g, bound, st)
+            : launch_doc_chunk_v<T, 4, false>(a, g, bound, st);
+}
+
+static int run_doc_chunks(const FwdArgs& a, maxsim_dtype dtype, void* workspace,
+                          hipStream_t st) {
+  const int64_t bound = doc_chunk_bound(a.nd, a.npairs);
+  DocChunks g;
+  g.chunks = static_cast<int2*>(workspace);
+  g.nchunks = reinterpret_cast<int32_t*>(g.chunks + bound);
+  g.dlist = g.nchunks + 2;
+  g.dstart = g.dlist + a.npairs;
+  g.dcur = g.dstart + a.nd + 1;
+  g.cpos = g.dcur + a.nd;
+  // one workgroup counts and scans (9 bytes of LDS per document) ...
+  const size_t glds = (size_t)a.nd * (2 * sizeof(int32_t) + 1);
+  if (glds > 64 * 1024) {
+    static std::atomic<bool> raised[kMaxDevices];
+    if (int e = raise_lds_limit((const void*)group_docs_kernel, glds, "group_docs_kernel", raised))
+      return e;
+  }
+  hipLaunchKernelGGL(group_docs_kernel, dim3(1), dim3(kDocGroupThreads), glds, st, a, g);
+  // ... and the chip scatters the pair ids and the chunk table
+  const int64_t n = std::max<int64_t>(a.npairs, a.nd);
+  const int64_t sgrid = std::min<int64_t>((n + 255) / 256, 4 * (int64_t)device_cus());
+  hipLaunchKernelGGL(scatter_docs_kernel, dim3((unsigned)sgrid), dim3(256), 0, st, a, g);
+  if (int e = check_launch("group_docs_kernel / scatter_docs_kernel")) return e;
+  const int rc = dtype == MAXSIM_BFLOAT16 ? launch_doc_chunk<BF16>(a, g, bound, st)
+                                          : launch_doc_chunk<F16>(a, g, bound, st);
+  if (rc) return rc;
+  return check_launch("doc_chunk_kernel");
 }
 
 static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
@@ -1366,14 +2016,14 @@ int maxsim_amd_padded_forward(maxsim_dtype dtype, const void* queries,
       num_candidates, Lq_max, Ld_max, dim, scores, nullptr, stream);
 }
 
-int maxsim_amd_packed_forward_with_argmax(
+static int packed_forward_impl(
     maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
     const int32_t* query_offsets, int64_t num_queries, const void* documents,
     int64_t total_d_tokens, const int32_t* document_offsets,
     int64_t num_documents, const int32_t* pair_query_ids,
     const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
-    int64_t max_q_len, float* scores, int32_t* argmax, void* stream) {
-  clear_error();
+    int64_t max_q_len, float* scores, int32_t* argmax, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (int e = check_dtype(dtype)) return e;
   if (total_q_tokens < 0 || num_queries < 0 || total_d_tokens < 0 ||
       num_documents < 0 || num_pairs < 0)
@@ -1411,7 +2061,46 @@ int maxsim_amd_packed_forward_with_argmax(
   a.total_d = total_d_tokens;
   a.scores = scores;
   a.argmax = argmax;
-  return run_pair(a, dtype, (int)max_q_len, static_cast<hipStream_t>(stream));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 7u) == 0 &&
+      workspace_bytes >= doc_chunk_ws_bytes(num_documents, num_pairs) &&
+      doc_chunk_fits(a, dtype, (int)max_q_len))
+    return run_doc_chunks(a, dtype, workspace, st);
+  return run_pair(a, dtype, (int)max_q_len, st);
+}
+
+int maxsim_amd_packed_forward_with_argmax(
+    maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
+    const int32_t* query_offsets, int64_t num_queries, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* pair_query_ids,
+    const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
+    int64_t max_q_len, float* scores, int32_t* argmax, void* stream) {
+  clear_error();
+  return packed_forward_impl(dtype, queries, total_q_tokens, query_offsets, num_queries,
+                             documents, total_d_tokens, document_offsets, num_documents,
+                             pair_query_ids, pair_document_ids, num_pairs, dim, max_q_len,
+                             scores, argmax, nullptr, 0, stream);
+}
+
+size_t maxsim_amd_packed_forward_workspace_size(int64_t num_documents, int64_t num_pairs) {
+  if (num_documents < 0 || num_pairs < 0) return 0;
+  return doc_chunk_ws_bytes(num_documents, num_pairs);
+}
+
+int maxsim_amd_packed_forward_with_argmax_ws(
+    maxsim_dtype dtype, const void* queries, int64_t total_q_tokens,
+    const int32_t* query_offsets, int64_t num_queries, const void* documents,
+    int64_t total_d_tokens, const int32_t* document_offsets,
+    int64_t num_documents, const int32_t* pair_query_ids,
+    const int32_t* pair_document_ids, int64_t num_pairs, int64_t dim,
+    int64_t max_q_len, float* scores, int32_t* argmax, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  clear_error();
+  return packed_forward_impl(dtype, queries, total_q_tokens, query_offsets, num_queries,
+                             documents, total_d_tokens, document_offsets, num_documents,
+                             pair_query_ids, pair_document_ids, num_pairs, dim, max_q_len,
+                             scores, argmax, workspace, workspace_bytes, stream);
 }
 
 int maxsim_amd_forward(maxsim_dtype dtype, const void* queries,

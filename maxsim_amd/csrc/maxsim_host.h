@@ -80,4 +80,26 @@ inline int raise_lds_limit(const void* kern, size_t bytes, const char* what,
   return MAXSIM_OK;
 }
 
+// Workgroups of `kern` (with `threads` threads and `lds` bytes of dynamic
+// LDS) that one CU holds at once, cached per device in the calling
+// instantiation's own array; 1 if the runtime cannot tell.
+inline int resident_per_cu(const void* kern, int threads, size_t lds,
+                           std::atomic<int> (&cached)[kMaxDevices]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  int v = dev < kMaxDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (v == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, threads, lds) != hipSuccess ||
+        v <= 0) {
+      (void)hipGetLastError();
+      v = 1;
+    }
+    if (dev < kMaxDevices) cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 }  // namespace maxsim

@@ -142,6 +142,12 @@ Packed prep_packed(Tensor queries, Tensor query_offsets, Tensor documents,
   return p;
 }
 
+// Device workspace (bytes) of maxsim_amd_packed_forward_with_argmax_ws.
+Tensor packed_forward_workspace(const Packed& p, int64_t np) {
+  const size_t bytes = maxsim_amd_packed_forward_workspace_size(p.doff.numel() - 1, np);
+  return at::empty({(int64_t)bytes}, p.q.options().dtype(at::kByte));
+}
+
 Tensor maxsim_forward(Tensor queries, Tensor query_offsets, Tensor documents,
                       Tensor document_offsets, Tensor pair_query_ids,
                       Tensor pair_document_ids, int64_t max_q_len) {
@@ -151,11 +157,15 @@ Tensor maxsim_forward(Tensor queries, Tensor query_offsets, Tensor documents,
   Tensor scores = at::empty({np}, f32_opts(p.q));
   if (np == 0) return scores;
   c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
-  check_status(maxsim_amd_forward(
+  // workspace for scoring the pairs document by document (see
+  // maxsim_amd_packed_forward_workspace_size)
+  Tensor ws = packed_forward_workspace(p, np);
+  check_status(maxsim_amd_packed_forward_with_argmax_ws(
       to_dtype(p.q), p.q.data_ptr(), p.q.size(0), p.qoff.data_ptr<int32_t>(),
       p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0), p.doff.data_ptr<int32_t>(),
       p.doff.numel() - 1, p.qids.data_ptr<int32_t>(), p.dids.data_ptr<int32_t>(), np,
-      p.q.size(1), p.mql, scores.data_ptr<float>(), current_stream(p.q)));
+      p.q.size(1), p.mql, scores.data_ptr<float>(), nullptr, ws.data_ptr(),
+      (size_t)ws.numel(), current_stream(p.q)));
   return scores;
 }
 
@@ -170,12 +180,13 @@ std::tuple<Tensor, Tensor> maxsim_packed_forward_with_argmax(
   Tensor argmax = at::empty({np, p.mql}, i32_opts(p.q));
   if (np == 0) return {scores, argmax};
   c10::hip::HIPGuardMasqueradingAsCUDA guard(p.q.device());
-  check_status(maxsim_amd_packed_forward_with_argmax(
+  Tensor ws = packed_forward_workspace(p, np);
+  check_status(maxsim_amd_packed_forward_with_argmax_ws(
       to_dtype(p.q), p.q.data_ptr(), p.q.size(0), p.qoff.data_ptr<int32_t>(),
       p.qoff.numel() - 1, p.d.data_ptr(), p.d.size(0), p.doff.data_ptr<int32_t>(),
       p.doff.numel() - 1, p.qids.data_ptr<int32_t>(), p.dids.data_ptr<int32_t>(), np,
       p.q.size(1), p.mql, scores.data_ptr<float>(), argmax.data_ptr<int32_t>(),
-      current_stream(p.q)));
+      ws.data_ptr(), (size_t)ws.numel(), current_stream(p.q)));
   return {scores, argmax};
 }
 

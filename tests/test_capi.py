@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declares_the_nine_ops_plus_helpers():
     names = declared_functions()
-    assert len(names) == 20, names
+    assert len(names) == 22, names
     for op in ["forward", "packed_forward_with_argmax", "packed_backward", "padded_forward",
                "padded_forward_with_argmax", "padded_backward", "contrastive_forward",
                "contrastive_forward_with_argmax", "contrastive_backward"]:
@@ -49,7 +49,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.maxsim_amd_abi_version() == 9
+    assert lib.maxsim_amd_abi_version() == 10
 
 
 def test_contrastive_backward_workspace_size(lib):
@@ -73,6 +73,19 @@ def test_packed_backward_workspace_size(lib):
     assert fn(512, 8192, 20000) == 4 * (2 * 512 + 1 + 2 * 8192 + 1 + 2 * 20000)
     assert fn(0, 0, 0) == 8
     assert fn(-1, 4, 4) == 0
+
+
+def test_packed_forward_workspace_size(lib):
+    fn = lib.maxsim_amd_packed_forward_workspace_size
+    fn.restype = ctypes.c_size_t
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    # chunks (int2) for ceil(P / 4) + min(nd, P) chunks, the chunk count
+    # (8 bytes), then int32: the pair ids grouped by document, run starts
+    # (nd + 1), run cursors and first chunks (nd each)
+    assert fn(8192, 20000) == 8 * (5000 + 8192) + 8 + 4 * 20000 + 4 * (3 * 8192 + 1)
+    assert fn(3, 4097) == 8 * (1025 + 3) + 8 + 4 * 4097 + 4 * 10
+    assert fn(0, 0) == 12
+    assert fn(-1, 4) == 0 and fn(4, -1) == 0
 
 
 I64 = ctypes.c_int64
