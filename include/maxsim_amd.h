@@ -92,16 +92,16 @@ int maxsim_amd_packed_forward_with_argmax(
     int64_t max_q_len, float* scores, int32_t* argmax, void* stream);
 
 /* Bytes of device workspace that let maxsim_amd_packed_forward_with_argmax_ws
- * score the pairs document by document: 8 * (ceil(num_pairs / 4) +
- * min(num_documents, num_pairs)) + 8 + 4 * num_pairs + 4 * (3 * num_documents
- * + 1).  No counterpart in the reference, whose packed forward scores the
- * pairs in the caller's order. */
+ * score the pairs document by document: 64 * (ceil(num_pairs / 4) +
+ * min(num_documents, num_pairs)) + 16 + 12 * num_documents.  No counterpart
+ * in the reference, whose packed forward scores the pairs in the caller's
+ * order. */
 size_t maxsim_amd_packed_forward_workspace_size(int64_t num_documents, int64_t num_pairs);
 
 /* Replaces ops `maxsim_packed_forward_with_argmax` (torch_binding.h:101-108,
  * maxsim.cu:2039-2108) and, with argmax NULL, `maxsim_forward`
  * (torch_binding.h:21-27), like the two entry points above, with a
- * workspace (device memory, 8-byte aligned, at least
+ * workspace (device memory, 16-byte aligned, at least
  * maxsim_amd_packed_forward_workspace_size() bytes): the pairs are grouped by
  * document on the device and each document's rows are read from memory once
  * per four of its pairs rather than once per pair.  Taken for 16-bit inputs

@@ -1046,12 +1046,23 @@ constexpr int kDocGroupThreads = 1024;
 constexpr int kLenClasses = 64;               // sort keys: tile count, clamped
 constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 9 bytes per document
 
+// A chunk: the document's rows and, per pair slot, its pair, resolved by
+// scatter_docs_kernel; doc_chunk_kernel copies its chunks into LDS.
+struct ChunkMeta {
+  int d_row0;
+  int ld;                      // 0: the document's segment is invalid
+  int pad[2];
+  int p[kChunkPairs];          // pair id; -1: no pair in this slot
+  int q_row0[kChunkPairs];
+  int lq[kChunkPairs];         // 0: invalid pair (NaN score)
+};
+static_assert(sizeof(ChunkMeta) % 16 == 0, "chunks are copied as 16-byte pieces");
+
 struct DocChunks {
-  int2* chunks;      // [max chunks] (first index into dlist, pair count)
+  ChunkMeta* recs;   // [max chunks], sorted by their document's length class
   int32_t* nchunks;  // [1]
-  int32_t* dlist;    // [npairs] pair ids grouped by document
-  int32_t* dstart;   // [nd + 1] start of each document's run in dlist
-  int32_t* dcur;     // [nd] the runs' cursors
+  int32_t* cnt;      // [nd] pairs per document
+  int32_t* dcur;     // [nd] pairs of each document placed so far
   int32_t* cpos;     // [nd] each document's first chunk
 };
 
@@ -1069,23 +1080,21 @@ __device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p)
 }
 
 // group_docs_kernel (one workgroup): pairs per document (LDS counters),
-// each document's length class (LDS bytes), an exclusive scan of the counts
-// into each document's run in dlist, and each document's first chunk by a
-// counting sort over the length classes (LDS cursors).  Its outputs go out
-// in coalesced passes: a single CU writing scattered words is what costs
+// each document's length class (LDS bytes), and each document's first chunk
+// by a counting sort over the length classes (LDS cursors).  Its outputs go
+// out in coalesced passes: a single CU writing scattered words is what costs
 // here (about one cache line per clock), so the scattered writes -- the
-// chunk table and the pair ids -- are left to scatter_docs_kernel, which
-// spreads them over the chip.  The ids and offsets are loaded up front, in
-// independent batches: a one-workgroup kernel takes as long as its chain of
-// dependent round trips.  A pair whose document id is out of range is
-// written off here (NaN score, zero argmax row).  Chunk positions within a
-// class follow the atomics; no result depends on them.
+// chunk records -- are left to scatter_docs_kernel, which spreads them over
+// the chip.  The ids and offsets are loaded up front, in independent
+// batches: a one-workgroup kernel takes as long as its chain of dependent
+// round trips.  A pair whose document id is out of range is written off
+// here (NaN score, zero argmax row).  Chunk positions within a class follow
+// the atomics; no result depends on them.
 constexpr int kGroupPairBatch = 24;  // pair ids per thread per batch
 constexpr int kGroupDocBatch = 8;    // document extents per thread per batch
 __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a, DocChunks g) {
-  extern __shared__ int32_t cnt[];            // [nd] counts, then run starts
+  extern __shared__ int32_t cnt[];            // [nd] pairs per document
   __shared__ int32_t cls[kLenClasses];        // chunks per class, then cursors
-  __shared__ int32_t wtot[kDocGroupThreads / 64];
   static_assert(kLenClasses == 64, "one class per lane of wave 0");
   constexpr int UP = kGroupPairBatch, UD = kGroupDocBatch;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1169,97 +1178,93 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
 #pragma unroll
     for (int u = 0; u < UD; ++u) classify(d0 + u * kDocGroupThreads, o_lo[u], o_hi[u]);
   }
-
-  // 3. a run of documents per thread: exclusive scan of the pair counts over
-  //    the workgroup; wave 0 also scans the class counts
-  const int per = (nd + kDocGroupThreads - 1) / kDocGroupThreads;
-  const int lo = min(tid * per, nd), hi = min(lo + per, nd);
-  int run = 0;
-  for (int d = lo; d < hi; ++d) run += cnt[d];
-  int incl = run;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off);
-    if (lane >= off) incl += t;
-  }
-  if (lane == 63) wtot[wave] = incl;
   __syncthreads();
+
+  // 3. exclusive scan of the class counts (wave 0, one class per lane)
   if (wave == 0) {
-    int w = lane < kDocGroupThreads / 64 ? wtot[lane] : 0;
     const int cc = cls[lane];
     int ci = cc;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(w, off);
       const int u = __shfl_up(ci, off);
-      if (lane >= off) {
-        w += t;
-        ci += u;
-      }
+      if (lane >= off) ci += u;
     }
-    if (lane < kDocGroupThreads / 64) wtot[lane] = w;  // inclusive over waves
-    cls[lane] = ci - cc;                              // first chunk of the class
+    cls[lane] = ci - cc;  // first chunk of the class
     if (lane == 63) g.nchunks[0] = ci;
   }
   __syncthreads();
 
-  // 4. run starts (in place of the counts) and first chunks
-  int start = incl - run + (wave > 0 ? wtot[wave - 1] : 0);
-  for (int d = lo; d < hi; ++d) {
-    const int c = cnt[d];
-    cnt[d] = start;
-    if (c > 0) cpos[d] = atomicAdd(&cls[kls[d]], (c + kChunkPairs - 1) / kChunkPairs);
-    start += c;
-  }
-  __syncthreads();
-
-  // 5. coalesced copy-out: run starts (and the total after the last), the
-  //    scatter's cursors, first chunks
+  // 4. each document's first chunk, and the coalesced copy-out
   for (int d = tid; d < nd; d += kDocGroupThreads) {
-    const int s = cnt[d];
-    g.dstart[d] = s;
-    g.dcur[d] = s;
-    g.cpos[d] = cpos[d];
+    const int c = cnt[d];
+    g.cnt[d] = c;
+    g.dcur[d] = 0;
+    g.cpos[d] = c > 0 ? atomicAdd(&cls[kls[d]], (c + kChunkPairs - 1) / kChunkPairs) : 0;
   }
-  if (tid == kDocGroupThreads - 1) g.dstart[nd] = wtot[kDocGroupThreads / 64 - 1];
 }
 
-// scatter_docs_kernel (grid-stride, many workgroups): each pair id into its
-// document's run (global cursors), and each document's chunks into the
-// chunk table at its first chunk: (first index in dlist, up to kChunkPairs
-// pairs).  The order inside a run follows the atomics; no result depends
-// on it.
+// scatter_docs_kernel (grid-stride, many workgroups): the chunk records.
+// Each pair takes the next place of its document (global cursors), i.e.
+// slot k % 4 of the document's chunk k / 4, and writes its id and its query
+// rows there (query length 0 when the pair or its document is invalid);
+// each document writes its rows into its chunks and marks the slots past its
+// last pair empty.  The order of a document's pairs follows the atomics; no
+// result depends on it.
 __global__ __launch_bounds__(256) void scatter_docs_kernel(FwdArgs a, DocChunks g) {
   const int nd = (int)a.nd;
   const int64_t np = a.npairs;
   const int64_t n = np > nd ? np : nd;
+  auto doc_rows = [&](int64_t d, int& d0, int& ld) __attribute__((always_inline)) {
+    const int64_t ds = a.doff[d], de = a.doff[d + 1];
+    const bool ok = ds >= 0 && de > ds && de <= a.total_d;
+    d0 = ok ? (int)ds : 0;
+    ld = ok ? (int)(de - ds) : 0;
+  };
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     if (i < np) {
       const int32_t d = a.dids[i];
-      if (d >= 0 && d < nd) g.dlist[atomicAdd(&g.dcur[d], 1)] = (int32_t)i;
+      if (d >= 0 && d < nd) {
+        const int k = atomicAdd(&g.dcur[d], 1);
+        ChunkMeta& r = g.recs[g.cpos[d] + k / kChunkPairs];
+        const int j = k % kChunkPairs;
+        int d0, ld;
+        doc_rows(d, d0, ld);
+        int q0 = 0, lq = 0;
+        const int64_t qi = a.qids[i];
+        if (ld > 0 && qi >= 0 && qi < a.nq) {
+          const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
+          if (qs >= 0 && qe > qs && qe <= a.total_q && qe - qs <= a.slots) {
+            q0 = (int)qs;
+            lq = (int)(qe - qs);
+          }
+        }
+        r.p[j] = (int)i;
+        r.q_row0[j] = q0;
+        r.lq[j] = lq;
+      }
     }
     if (i < nd) {
-      const int s = g.dstart[i];
-      const int c = g.dstart[i + 1] - s;
+      const int c = g.cnt[i];
       if (c > 0) {
+        int d0, ld;
+        doc_rows(i, d0, ld);
         const int base = g.cpos[i];
-        for (int j = 0; j * kChunkPairs < c; ++j)
-          g.chunks[base + j] = make_int2(s + j * kChunkPairs, min(kChunkPairs, c - j * kChunkPairs));
+        const int nch = (c + kChunkPairs - 1) / kChunkPairs;
+        for (int jc = 0; jc < nch; ++jc) {
+          ChunkMeta& r = g.recs[base + jc];
+          r.d_row0 = d0;
+          r.ld = ld;
+        }
+        ChunkMeta& last = g.recs[base + nch - 1];
+        for (int j = c - (nch - 1) * kChunkPairs; j < kChunkPairs; ++j) {
+          last.p[j] = -1;
+          last.q_row0[j] = 0;
+          last.lq[j] = 0;
+        }
       }
     }
   }
 }
-
-// A chunk as the scoring workgroup sees it, resolved once into LDS before
-// any tile load: the document's rows and, per pair slot, its pair.
-struct ChunkMeta {
-  int d_row0;
-  int ld;                      // 0: the document's segment is invalid
-  int pad[2];
-  int p[kChunkPairs];          // pair id; -1: no pair in this slot
-  int q_row0[kChunkPairs];
-  int lq[kChunkPairs];         // 0: invalid pair (NaN score)
-};
 
 // LDS per workgroup of doc_chunk_kernel (ring + chunk metadata; 68 KB at
 // dim 128: two workgroups per CU), and the waves per SIMD its register
@@ -1302,8 +1307,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // and the loaders refill that slot.
 template <typename T, int KS, bool ARGMAX, bool STREAM>
 __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) void doc_chunk_kernel(
-    FwdArgs a, const int2* __restrict__ chunks, const int32_t* __restrict__ nchunks_p,
-    const int32_t* __restrict__ dlist) {
+    FwdArgs a, const ChunkMeta* __restrict__ recs, const int32_t* __restrict__ nchunks_p) {
   using S = typename T::storage;
   using G = TileGeom<T, KS>;
   static_assert(T::bytes == 2, "16-bit operands: one 16-byte piece per fragment");
@@ -1334,41 +1338,12 @@ __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) v
   const int dim = a.dim;
   const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(S);
 
-  // ---- chunk metadata: thread s resolves pair slot s % 4 of chunk s / 4;
-  // every index read from device memory is range-checked
-  for (int s = threadIdx.x; s < mine * kChunkPairs; s += kChunkWaves * 64) {
-    const int ci = s / kChunkPairs, j = s - ci * kChunkPairs;
-    const int2 ch = chunks[snake_chunk(b, ci, grid)];
-    int p = -1, q0 = 0, lq = 0, d0 = 0, ld = 0;
-    if (j < ch.y && ch.x + j >= 0 && ch.x + j < a.npairs) {
-      p = dlist[ch.x + j];
-      if (p < 0 || p >= a.npairs) p = -1;
-    }
-    if (p >= 0) {
-      const int64_t qi = a.qids[p], di = a.dids[p];
-      if (di >= 0 && di < a.nd) {
-        const int64_t ds = a.doff[di], de = a.doff[di + 1];
-        if (ds >= 0 && de > ds && de <= a.total_d) {
-          d0 = (int)ds;
-          ld = (int)(de - ds);
-          if (qi >= 0 && qi < a.nq) {
-            const int64_t qs = a.qoff[qi], qe = a.qoff[qi + 1];
-            if (qs >= 0 && qe > qs && qe <= a.total_q && qe - qs <= a.slots) {
-              q0 = (int)qs;
-              lq = (int)(qe - qs);
-            }
-          }
-        }
-      }
-    }
-    ChunkMeta& m = meta[ci];
-    m.p[j] = p;
-    m.q_row0[j] = q0;
-    m.lq[j] = lq;
-    if (j == 0) {
-      m.d_row0 = d0;
-      m.ld = ld;
-    }
+  // ---- chunk records into LDS, one 16-byte piece per thread
+  constexpr int kPieces16 = (int)sizeof(ChunkMeta) / 16;
+  for (int s = threadIdx.x; s < mine * kPieces16; s += kChunkWaves * 64) {
+    const int ci = s / kPieces16, part = s - ci * kPieces16;
+    reinterpret_cast<uint4*>(meta + ci)[part] =
+        reinterpret_cast<const uint4*>(recs + snake_chunk(b, ci, grid))[part];
   }
   __syncthreads();
 
@@ -1697,10 +1672,10 @@ static bool doc_chunk_fits(const FwdArgs& a, maxsim_dtype dtype, int max_lq) {
          a.npairs >= kDocChunkMinPairs && a.npairs <= INT32_MAX;
 }
 
-// Workspace: chunks (int2) [doc_chunk_bound], nchunks (int32, padded to 8
-// bytes), then int32 dlist [npairs], dstart [nd + 1], dcur [nd], cpos [nd].
+// Workspace: chunk records (64 bytes) [doc_chunk_bound], nchunks (int32,
+// padded to 16 bytes), then int32 cnt [nd], dcur [nd], cpos [nd].
 static size_t doc_chunk_ws_bytes(int64_t nd, int64_t npairs) {
-  return 8 * (size_t)doc_chunk_bound(nd, npairs) + 8 + 4 * (size_t)npairs + 4 * (3 * (size_t)nd + 1);
+  return sizeof(ChunkMeta) * (size_t)doc_chunk_bound(nd, npairs) + 16 + 12 * (size_t)nd;
 }
 
 // Grid: as many workgroups as the chip holds at once (LDS or registers
@@ -1721,8 +1696,7 @@ static int launch_doc_chunk_v(const FwdArgs& a, const DocChunks& g, int64_t boun
       (int64_t)device_cus() * resident_per_cu((const void*)kern, kChunkWaves * 64, lds, per_cu);
   const int64_t grid = std::max<int64_t>(resident, (bound + kChunkBatch - 1) / kChunkBatch);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kChunkWaves * 64), lds, st, a,
-                     static_cast<const int2*>(g.chunks), static_cast<const int32_t*>(g.nchunks),
-                     static_cast<const int32_t*>(g.dlist));
+                     static_cast<const ChunkMeta*>(g.recs), static_cast<const int32_t*>(g.nchunks));
   return MAXSIM_OK;
 }
 
@@ -1741,11 +1715,10 @@ static int run_doc_chunks(const FwdArgs& a, maxsim_dtype dtype, void* workspace,
                           hipStream_t st) {
   const int64_t bound = doc_chunk_bound(a.nd, a.npairs);
   DocChunks g;
-  g.chunks = static_cast<int2*>(workspace);
-  g.nchunks = reinterpret_cast<int32_t*>(g.chunks + bound);
-  g.dlist = g.nchunks + 2;
-  g.dstart = g.dlist + a.npairs;
-  g.dcur = g.dstart + a.nd + 1;
+  g.recs = static_cast<ChunkMeta*>(workspace);
+  g.nchunks = reinterpret_cast<int32_t*>(g.recs + bound);
+  g.cnt = g.nchunks + 4;
+  g.dcur = g.cnt + a.nd;
   g.cpos = g.dcur + a.nd;
   // one workgroup counts and scans (9 bytes of LDS per document) ...
   const size_t glds = (size_t)a.nd * (2 * sizeof(int32_t) + 1);
@@ -2062,7 +2035,7 @@ static int packed_forward_impl(
   a.scores = scores;
   a.argmax = argmax;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 7u) == 0 &&
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0 &&
       workspace_bytes >= doc_chunk_ws_bytes(num_documents, num_pairs) &&
       doc_chunk_fits(a, dtype, (int)max_q_len))
     return run_doc_chunks(a, dtype, workspace, st);

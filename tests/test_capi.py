@@ -79,12 +79,12 @@ def test_packed_forward_workspace_size(lib):
     fn = lib.maxsim_amd_packed_forward_workspace_size
     fn.restype = ctypes.c_size_t
     fn.argtypes = [ctypes.c_int64, ctypes.c_int64]
-    # chunks (int2) for ceil(P / 4) + min(nd, P) chunks, the chunk count
-    # (8 bytes), then int32: the pair ids grouped by document, run starts
-    # (nd + 1), run cursors and first chunks (nd each)
-    assert fn(8192, 20000) == 8 * (5000 + 8192) + 8 + 4 * 20000 + 4 * (3 * 8192 + 1)
-    assert fn(3, 4097) == 8 * (1025 + 3) + 8 + 4 * 4097 + 4 * 10
-    assert fn(0, 0) == 12
+    # 64-byte chunk records for ceil(P / 4) + min(nd, P) chunks, the chunk
+    # count (16 bytes), then int32 per document: pairs, placed pairs, first
+    # chunk
+    assert fn(8192, 20000) == 64 * (5000 + 8192) + 16 + 12 * 8192
+    assert fn(3, 4097) == 64 * (1025 + 3) + 16 + 12 * 3
+    assert fn(0, 0) == 16
     assert fn(-1, 4) == 0 and fn(4, -1) == 0
 
 
