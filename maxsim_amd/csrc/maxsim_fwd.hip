@@ -1039,11 +1039,19 @@ constexpr int kChunkWaves = kChunkLoaders + kChunkSets * kChunkPairs;
 // (C4 forward 124-131 us; 147-155 at depth 6 and three per CU, 179 at depth
 // 8 and one per CU, 168-192 with two loader waves)
 constexpr int kChunkSlots = 8;
+// Tiles per barrier: with two, the pair waves take two tiles between
+// barriers and the loader refills two slots after each; C4 forward 133.0
+// against 133.7 us with one, i.e. the barriers are not what bounds it.
+constexpr int kTilesPerBarrier = 1;
 
 
 constexpr int kChunkBatch = 64;               // chunks per workgroup, at most
 constexpr int kDocGroupThreads = 1024;
-constexpr int kLenClasses = 64;               // sort keys: tile count, clamped
+// Sort keys: 4 * (63 - the document's tile count, clamped) + the low two
+// bits of its id -- longest first; the id bits only spread the atomics of
+// documents of one length over four counters (C4's lengths fall into a few
+// tile counts, and same-address LDS atomics serialise)
+constexpr int kLenClasses = 256;
 constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 9 bytes per document
 
 // A chunk: the document's rows and, per pair slot, its pair, resolved by
@@ -1095,7 +1103,7 @@ constexpr int kGroupDocBatch = 8;    // document extents per thread per batch
 __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a, DocChunks g) {
   extern __shared__ int32_t cnt[];            // [nd] pairs per document
   __shared__ int32_t cls[kLenClasses];        // chunks per class, then cursors
-  static_assert(kLenClasses == 64, "one class per lane of wave 0");
+  static_assert(kLenClasses == 4 * 64, "four classes per lane of wave 0");
   constexpr int UP = kGroupPairBatch, UD = kGroupDocBatch;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nd = (int)a.nd;
@@ -1161,7 +1169,7 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
     if (d >= nd) return;
     const int64_t ld = (int64_t)hi_off - lo_off;
     const int64_t t = ld <= 0 ? 0 : (ld + kTileRows - 1) / kTileRows;
-    const int k = kLenClasses - 1 - (int)(t < kLenClasses - 1 ? t : kLenClasses - 1);
+    const int k = 4 * (63 - (int)(t < 63 ? t : 63)) + (d & 3);
     kls[d] = (uint8_t)k;
     const int c = cnt[d];
     if (c > 0) atomicAdd(&cls[k], (c + kChunkPairs - 1) / kChunkPairs);
@@ -1180,16 +1188,27 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
   }
   __syncthreads();
 
-  // 3. exclusive scan of the class counts (wave 0, one class per lane)
+  // 3. exclusive scan of the class counts (wave 0, four classes per lane)
   if (wave == 0) {
-    const int cc = cls[lane];
-    int ci = cc;
+    int c4[4];
+    int run = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      c4[u] = cls[4 * lane + u];
+      run += c4[u];
+    }
+    int ci = run;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int u = __shfl_up(ci, off);
       if (lane >= off) ci += u;
     }
-    cls[lane] = ci - cc;  // first chunk of the class
+    int first = ci - run;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      cls[4 * lane + u] = first;  // first chunk of the class
+      first += c4[u];
+    }
     if (lane == 63) g.nchunks[0] = ci;
   }
   __syncthreads();
@@ -1316,7 +1335,9 @@ __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) v
   constexpr int kDma = G::kPieces / 64;           // wave load instructions per tile
   constexpr int kDmaL = kDma / kChunkLoaders;     // ... issued by each loader
   static_assert(kDma % kChunkLoaders == 0 && kDmaL >= 1, "tile loads split evenly");
-  static_assert(kDmaL * (kChunkSlots - 1) <= 63, "a loader's tiles in flight fit vmcnt");
+  static_assert(kDmaL * (kChunkSlots - kTilesPerBarrier) <= 63,
+                "a loader's tiles in flight fit vmcnt");
+  static_assert(kChunkSlots > 2 * kTilesPerBarrier, "a ring deeper than two steps");
   extern __shared__ uint4 lds[];
   ChunkMeta* meta = reinterpret_cast<ChunkMeta*>(lds + kChunkSlots * G::kBufPieces);
   const int lane = threadIdx.x & 63;
@@ -1422,14 +1443,21 @@ __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) v
         default: wait_vmcnt<0>(); break;
       }
     };
-    for (int i = 0; i < kChunkSlots - 1; ++i) load_next();
+    // Barrier before tile k when k % kTilesPerBarrier == 0: tiles k ..
+    // k + kTilesPerBarrier - 1 have landed, and the pair waves have read the
+    // slots of the kTilesPerBarrier tiles before k, which the loads issued
+    // after the barrier refill.
+    for (int i = 0; i < kChunkSlots - kTilesPerBarrier; ++i) load_next();
     int k = 0;
     for (int ci = 0; ci < mine; ++ci) {
       const int nt = chunk_tiles(ci);
       for (int t = 0; t < nt; ++t, ++k) {
-        wait_tile(issued - k - 1);
-        barrier();
-        load_next();  // into the slot of tile k - 1, which no wave reads any more
+        if (k % kTilesPerBarrier == 0) {
+          wait_tile(issued - k - kTilesPerBarrier);
+          barrier();
+#pragma unroll
+          for (int i = 0; i < kTilesPerBarrier; ++i) load_next();
+        }
       }
     }
     // drain: no load may still be writing LDS when the wave exits
@@ -1466,12 +1494,14 @@ __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) v
   };
   if (set < mine) load_query(set);
   int cslot = 0;  // slot of the next tile
+  int kk = 0;     // the next tile's place in the workgroup's tile stream
   for (int ci = 0; ci < mine; ++ci) {
     const int nt = chunk_tiles(ci);
     if (ci % kChunkSets != set) {
       // the other set's chunk: keep the barriers
       for (int t = 0; t < nt; ++t) {
-        barrier();
+        if (kk % kTilesPerBarrier == 0) barrier();
+        ++kk;
         if (++cslot == kChunkSlots) cslot = 0;
       }
       continue;
@@ -1490,9 +1520,12 @@ __global__ __launch_bounds__(kChunkWaves * 64, (ChunkOcc<T, KS>::kWavesPerEu)) v
     auto walk = [&](auto na_const) __attribute__((always_inline)) {
       constexpr int NA = decltype(na_const)::value;
       auto tile_step = [&](int t) __attribute__((always_inline)) {
-        // this wave's reads of the previous tile have returned
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        barrier();
+        if (kk % kTilesPerBarrier == 0) {
+          // this wave's reads of the tiles before have returned
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          barrier();
+        }
+        ++kk;
         if constexpr (NA > 0) {
           const uint4* tile = lds + cslot * G::kBufPieces;
           Frag<T> df[KS];
