@@ -225,7 +225,8 @@ def cpu_median(fn, reps, warmup):
 
 def profile_ops(torch, dev):
     """The C5 operators in isolation (3x forward with argmax, 3x the fp32
-    backward operator, 3x the typed backward of the training step), then two
+    backward operator, 3x the typed backward of the training step), the C4
+    packed forward (3x document-major, 3x pair kernel), then two
     of this build's own kernels whose HBM bytes are known exactly, to
     calibrate the FETCH_SIZE / WRITE_SIZE counters to bytes:
 
@@ -246,6 +247,26 @@ def profile_ops(torch, dev):
     for _ in range(3):
         ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
     del q, d, scores, argmax
+    # C4 packed forward: 3x through the operator (document-major: grouping,
+    # then doc_chunk_kernel), 3x through the C ABI entry point without a
+    # workspace (pair_ring_kernel), the path C4 took before
+    (q4, qo4, d4, do4, qi4, di4, mql, *_rest) = make_c4(torch, dev)
+    for _ in range(3):
+        ops.maxsim_packed_forward_with_argmax(q4, qo4, d4, do4, qi4, di4, mql)
+    import ctypes
+    from maxsim_amd._ops import NATIVE_LIB
+    fn = ctypes.CDLL(str(NATIVE_LIB)).maxsim_amd_packed_forward_with_argmax
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    fn.argtypes = [ctypes.c_int, P, I64, P, I64, P, I64, P, I64, P, P, I64, I64, I64, P, P, P]
+    s4 = torch.empty(qi4.numel(), device=dev)
+    a4 = torch.empty(qi4.numel(), mql, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        rc = fn(2, q4.data_ptr(), q4.shape[0], qo4.data_ptr(), qo4.numel() - 1, d4.data_ptr(),
+                d4.shape[0], do4.data_ptr(), do4.numel() - 1, qi4.data_ptr(), di4.data_ptr(),
+                qi4.numel(), q4.shape[1], mql, s4.data_ptr(), a4.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, rc
+    del q4, d4, s4, a4
     # calibration 1: a 1 GiB row copy through pack_rows_kernel
     seg, ld, dim = 4096, 1024, 128
     padded = torch.randn(seg * ld, dim, device=dev).to(torch.bfloat16)
