@@ -373,7 +373,6 @@ __global__ __launch_bounds__(256) void dq_gather_kernel(DqArgs a, bool vec) {
 // between batches.  Documents are added in order, one FMA each (weight 0 for
 // an invalid entry).
 // ---------------------------------------------------------------------------
-constexpr int kXcds = 8;
 constexpr int kDqBatch = 4;
 constexpr int kDqSplitMaxDim = 2048;  // 8 * 256 slices: one row per workgroup at most
 constexpr int kDqTable = 2048;  // (row, document) pairs staged per chunk

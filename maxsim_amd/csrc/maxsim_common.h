@@ -30,6 +30,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileRows = 32;   // document rows per MFMA tile
 constexpr int kTileCols = 32;   // query tokens per MFMA tile (one "query block")
+// gfx950 dispatches workgroup w to XCD w % kXcds; each XCD has its own L2
+constexpr int kXcds = 8;
 constexpr int kChunk = 16;      // embedding elements per K-chunk
 
 // Element tags (storage is raw bits; arithmetic happens inside MFMA).

@@ -338,8 +338,16 @@ __global__ __launch_bounds__(256) void wide_pair_kernel(FwdArgs a) {
 constexpr int kTiledWaves = 8;
 constexpr int kTiledThreads = kTiledWaves * 64;
 constexpr int kTileBuffers = 4;        // LDS tile ring
-constexpr int kMaxDocsPerGroup = 2048;  // LDS offset table per workgroup
+constexpr int kMaxDocsPerGroup = 2048;  // LDS document list per workgroup
+constexpr int kDocTableBytes = 3 * (int)sizeof(int) * kMaxDocsPerGroup;  // rows, end, id
 constexpr int kDocWork = 32;            // work of a document beyond its rows, in rows
+constexpr int kLptKeys = 128;           // sort keys of the dealt lists: tile counts, clamped
+// Dealt lists when chunks average fewer documents than this: with 8 per
+// chunk (64 queries x 512 C5 documents) contiguous chunks of whole documents
+// hold up to 17 % more tiles than the mean (forward 139.6 -> 128.4 us
+// dealt); with 64 (C5) within 2 %, and the ranking costs more (952.7 against
+// 955 us)
+constexpr int kDealtBelowDocsPerChunk = 32;
 
 struct TiledArgs {
   const void* q;
@@ -388,10 +396,11 @@ struct TileGeom {
 // wave-uniform 32-bit values (document offsets are int32), so the walk stays
 // in scalar registers.
 struct TileCursor {
-  int b;          // document, relative to the workgroup's first
+  int b;          // entry of the workgroup's document list
   int row0;       // its first row
   int ld;         // its length (0 when past the end)
   int t;          // tile within the document
+  int id;         // its document index
 };
 
 template <typename T, int KS, int NBW, bool ARGMAX>
@@ -435,45 +444,180 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       qf[j][s] = load_frag<T>(row, kChunk * s + 8 * h, dim, true);
   }
 
-  // Document chunk dc: the documents whose work prefix W(b) = off[b] +
-  // kDocWork * b falls in [dc, dc + 1) * W / n_dc, W = total_d + kDocWork *
-  // nb (rows, plus one tile's worth per document for its last partial tile
-  // and its document-end work), so chunks hold equal work, not equal counts.
-  // The bounds are counts of documents below each threshold, one parallel
-  // pass over the offsets; counts partition [0, nb) for any offsets.
-  __shared__ int chunk_cnt[2];
-  if (threadIdx.x < 2) chunk_cnt[threadIdx.x] = 0;
-  __syncthreads();
-  if (a.n_dc >= a.nb) {
-    // one document per chunk: nothing to balance
-    if (threadIdx.x == 0) {
-      chunk_cnt[0] = dc;
-      chunk_cnt[1] = (int)min((int64_t)dc + 1, a.nb);
-    }
-  } else {
-    const int64_t w_all = a.total_d + (int64_t)kDocWork * a.nb;
-    const int64_t w_lo = w_all * dc / a.n_dc;
-    const int64_t w_hi = w_all * (dc + 1) / a.n_dc;
-    int c_lo = 0, c_hi = 0;
-    for (int64_t bb = threadIdx.x; bb < a.nb; bb += kTiledThreads) {
-      const int64_t w = (int64_t)a.doff[bb] + (int64_t)kDocWork * bb;
-      c_lo += w < w_lo ? 1 : 0;
-      c_hi += w < w_hi ? 1 : 0;
-    }
-    if (c_lo) atomicAdd(&chunk_cnt[0], c_lo);
-    if (c_hi) atomicAdd(&chunk_cnt[1], c_hi);
-  }
-  __syncthreads();
-  const int64_t b_begin = dc == 0 ? 0 : chunk_cnt[0];
-  const int64_t b_end = dc == a.n_dc - 1 ? a.nb : chunk_cnt[1];
+  // The documents of chunk dc, as a list in LDS (rows [s, e) and index of
+  // entry bl).  Two ways to form the chunks:
+  //  * dealt (more than one chunk, fewer than kDealtBelowDocsPerChunk
+  //    documents per chunk on average, at most one document per thread):
+  //    the documents sorted by tile count, longest
+  //    first (ties by index), and dealt in snake order, place p of round r
+  //    to chunk p (r even) or n_dc - 1 - p (r odd), so every chunk gets a
+  //    near-equal share of the tiles whatever the lengths.  Every workgroup
+  //    ranks all documents itself (the same ranks everywhere): one thread
+  //    per document, ranks within a wave by ballot (a pass per distinct key
+  //    in the wave), counts per wave and key in LDS;
+  //  * contiguous: the documents whose work prefix W(b) = off[b] + kDocWork
+  //    * b falls in [dc, dc + 1) * W / n_dc, W = total_d + kDocWork * nb
+  //    (rows, plus one tile's worth per document for its last partial tile
+  //    and its document-end work), so chunks hold equal work, not equal
+  //    counts.  The bounds are counts of documents below each threshold, one
+  //    parallel pass over the offsets; counts partition [0, nb) for any
+  //    offsets.
   float* __restrict__ scores = a.scores;
   int32_t* __restrict__ argmax_out = a.argmax;
-  // With non-decreasing offsets consecutive documents are kDocWork apart in
-  // W, so the host's chunk count keeps every chunk within the offset table.
-  // Only offsets that decrease or overrun total_d can break that; such a
-  // chunk is reported like documents with invalid offsets.
-  if (b_end - b_begin > kMaxDocsPerGroup) {
-    for (int64_t b = b_begin; b < b_end; ++b) {
+  int* tab_s = reinterpret_cast<int*>(lds + kTileBuffers * G::kBufPieces);
+  int* tab_e = tab_s + kMaxDocsPerGroup;
+  int* tab_id = tab_e + kMaxDocsPerGroup;
+  int n_docs = 0;
+  if (a.n_dc > 1 && a.n_dc < a.nb && a.nb <= kTiledThreads &&
+      a.nb < (int64_t)kDealtBelowDocsPerChunk * a.n_dc) {
+    // scratch in the tile ring, which no load has touched yet
+    static_assert((kTiledWaves + 1) * kLptKeys * (int)sizeof(int) <=
+                      kTileBuffers * G::kBufPieces * (int)sizeof(uint4),
+                  "ranking scratch fits the tile ring");
+    int* kcnt = reinterpret_cast<int*>(lds);       // [wave][key] counts, then waves-before
+    int* kfirst = kcnt + kTiledWaves * kLptKeys;   // [key] first rank
+    for (int i = tid; i < kTiledWaves * kLptKeys; i += kTiledThreads) kcnt[i] = 0;
+    const bool own = tid < a.nb;
+    int s0 = 0, e0 = 0, key = 0;
+    if (own) {
+      s0 = a.doff[tid];
+      e0 = a.doff[tid + 1];
+      const bool ok = (s0 >= 0) && (e0 > s0) && ((int64_t)e0 <= a.total_d);
+      const int t = ok ? (e0 - s0 + kTileRows - 1) / kTileRows : 0;
+      key = t < kLptKeys - 1 ? t : kLptKeys - 1;
+    }
+    __syncthreads();
+    // rank among the wave's lanes of equal key, and each key's count
+    uint64_t rem = __ballot(own);
+    int pos = 0;
+    while (rem) {
+      const int l0 = __ffsll((unsigned long long)rem) - 1;
+      const int k0 = __shfl(key, l0);
+      const uint64_t mk = __ballot(own && key == k0);
+      if (own && key == k0) pos = __popcll(mk & ((1ull << lane) - 1ull));
+      if (lane == l0) kcnt[wave * kLptKeys + k0] = __popcll(mk);
+      rem &= ~mk;
+    }
+    __syncthreads();
+    // per key (wave 0, two keys per lane, largest first): the counts of the
+    // waves before each wave, and the key's first rank, the total of the
+    // larger keys
+    static_assert(kLptKeys == 2 * 64, "two keys per lane of wave 0");
+    if (wave == 0) {
+      const int ka = kLptKeys - 1 - 2 * lane, kb = ka - 1;
+      int ca[kTiledWaves], cb[kTiledWaves];
+#pragma unroll
+      for (int w = 0; w < kTiledWaves; ++w) {
+        ca[w] = kcnt[w * kLptKeys + ka];
+        cb[w] = kcnt[w * kLptKeys + kb];
+      }
+      int ta = 0, tb = 0;
+#pragma unroll
+      for (int w = 0; w < kTiledWaves; ++w) {
+        kcnt[w * kLptKeys + ka] = ta;
+        kcnt[w * kLptKeys + kb] = tb;
+        ta += ca[w];
+        tb += cb[w];
+      }
+      int ci = ta + tb;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(ci, o);
+        if (lane >= o) ci += u;
+      }
+      kfirst[ka] = ci - ta - tb;
+      kfirst[kb] = ci - tb;
+    }
+    __syncthreads();
+    const int nc = a.n_dc, nbd = (int)a.nb;
+    if (own) {
+      const int r = kfirst[key] + kcnt[wave * kLptKeys + key] + pos;
+      const int rd = r / nc, p = r - rd * nc;
+      if (((rd & 1) ? nc - 1 - p : p) == dc) {
+        tab_s[rd] = s0;
+        tab_e[rd] = e0;
+        tab_id[rd] = tid;
+      }
+    }
+    const int full = nbd / nc, tail = nbd - full * nc;
+    n_docs = full + (tail > 0 && ((full & 1) ? nc - 1 - dc : dc) < tail ? 1 : 0);
+  } else {
+    __shared__ int chunk_cnt[2];
+    if (threadIdx.x < 2) chunk_cnt[threadIdx.x] = 0;
+    __syncthreads();
+    if (a.n_dc >= a.nb) {
+      // one document per chunk: nothing to balance
+      if (threadIdx.x == 0) {
+        chunk_cnt[0] = dc;
+        chunk_cnt[1] = (int)min((int64_t)dc + 1, a.nb);
+      }
+    } else {
+      const int64_t w_all = a.total_d + (int64_t)kDocWork * a.nb;
+      const int64_t w_lo = w_all * dc / a.n_dc;
+      const int64_t w_hi = w_all * (dc + 1) / a.n_dc;
+      int c_lo = 0, c_hi = 0;
+      for (int64_t bb = threadIdx.x; bb < a.nb; bb += kTiledThreads) {
+        const int64_t w = (int64_t)a.doff[bb] + (int64_t)kDocWork * bb;
+        c_lo += w < w_lo ? 1 : 0;
+        c_hi += w < w_hi ? 1 : 0;
+      }
+      if (c_lo) atomicAdd(&chunk_cnt[0], c_lo);
+      if (c_hi) atomicAdd(&chunk_cnt[1], c_hi);
+    }
+    __syncthreads();
+    const int64_t b_begin = dc == 0 ? 0 : chunk_cnt[0];
+    const int64_t b_end = dc == a.n_dc - 1 ? a.nb : chunk_cnt[1];
+    // With non-decreasing offsets consecutive documents are kDocWork apart
+    // in W, so the host's chunk count keeps every chunk within the list.
+    // Only offsets that decrease or overrun total_d can break that; such a
+    // chunk is reported like documents with invalid offsets.
+    if (b_end - b_begin > kMaxDocsPerGroup) {
+      for (int64_t b = b_begin; b < b_end; ++b) {
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) {
+          const int64_t q = q_first + j / a.nblk;
+          if (j >= a.qpw * a.nblk || q >= a.nq) continue;
+          const int tok = (j % a.nblk) * kTileCols + c;
+          if (ARGMAX && argmax_out && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
+          if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
+        }
+      }
+      return;
+    }
+    n_docs = (int)(b_end - b_begin);
+    for (int i = tid; i < n_docs; i += kTiledThreads) {
+      tab_s[i] = a.doff[b_begin + i];
+      tab_e[i] = a.doff[b_begin + i + 1];
+      tab_id[i] = (int)(b_begin + i);
+    }
+  }
+  // The list is in LDS once, so the tile walk never issues global loads of
+  // its own: the only vector-memory loads in flight are the tile loads,
+  // whose completion is tracked by count.
+  __syncthreads();
+  // Offsets of local document bl (uniform: read back as scalars).
+  auto doc_ok = [&](int bl, int& s0, int& ld) {
+    const int s = __builtin_amdgcn_readfirstlane(tab_s[bl]);
+    const int e = __builtin_amdgcn_readfirstlane(tab_e[bl]);
+    s0 = s;
+    ld = e - s;
+    return (s >= 0) && (e > s) && ((int64_t)e <= a.total_d);
+  };
+  // One pass over the list, a lane per entry: the tiles to walk, and the
+  // documents with invalid offsets (NaN score, zero argmax, never read).
+  int ntiles = 0;
+  for (int bl0 = 0; bl0 < n_docs; bl0 += 64) {
+    const int bl = bl0 + lane;
+    bool bad = false;
+    if (bl < n_docs) {
+      const int s = tab_s[bl], e = tab_e[bl];
+      if ((s >= 0) && (e > s) && ((int64_t)e <= a.total_d))
+        ntiles += (e - s + kTileRows - 1) / kTileRows;
+      else
+        bad = true;
+    }
+    for (uint64_t mb = __ballot(bad); mb; mb &= mb - 1) {
+      const int64_t b = __builtin_amdgcn_readfirstlane(tab_id[bl0 + __ffsll((unsigned long long)mb) - 1]);
 #pragma unroll
       for (int j = 0; j < NBW; ++j) {
         const int64_t q = q_first + j / a.nblk;
@@ -483,43 +627,13 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
       }
     }
-    return;
   }
-  // The chunk's document offsets are copied to LDS once, so the tile walk
-  // never issues global loads of its own: the only vector-memory loads in
-  // flight are the tile loads, whose completion is tracked by count.
-  int* doff_lds = reinterpret_cast<int*>(lds + kTileBuffers * G::kBufPieces);
-  for (int64_t i = tid; i <= b_end - b_begin; i += kTiledThreads)
-    doff_lds[i] = a.doff[b_begin + i];
-  __syncthreads();
-
-  const int n_docs = (int)(b_end - b_begin);
-  // Offsets of local document bl (uniform: read back as scalars).
-  auto doc_ok = [&](int bl, int& s0, int& ld) {
-    const int s = __builtin_amdgcn_readfirstlane(doff_lds[bl]);
-    const int e = __builtin_amdgcn_readfirstlane(doff_lds[bl + 1]);
-    s0 = s;
-    ld = e - s;
-    return (s >= 0) && (e > s) && ((int64_t)e <= a.total_d);
-  };
-  // Documents with invalid offsets: NaN score, zero argmax, never read.
-  for (int bl = 0; bl < n_docs; ++bl) {
-    const int64_t b = b_begin + bl;
-    int s0;
-    int ld;
-    if (doc_ok(bl, s0, ld)) continue;
 #pragma unroll
-    for (int j = 0; j < NBW; ++j) {
-      const int64_t q = q_first + j / a.nblk;
-      if (j >= a.qpw * a.nblk || q >= a.nq) continue;
-      const int tok = (j % a.nblk) * kTileCols + c;
-      if (ARGMAX && argmax_out && h == 0 && tok < a.lq) argmax_out[(q * a.nb + b) * a.lq + tok] = 0;
-      if (j % a.nblk == 0 && lane == 0) scores[q * a.nb + b] = __builtin_nanf("");
-    }
-  }
+  for (int o = 32; o > 0; o >>= 1) ntiles += __shfl_xor(ntiles, o);
+  ntiles = __builtin_amdgcn_readfirstlane(ntiles);
   // First valid document at or after local index bl (cursor at its tile 0).
   auto seek = [&](int bl) -> TileCursor {
-    TileCursor cur{n_docs, 0, 0, 0};
+    TileCursor cur{n_docs, 0, 0, 0, 0};
     for (; bl < n_docs; ++bl) {
       int s0;
       int ld;
@@ -527,6 +641,7 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         cur.b = bl;
         cur.row0 = s0;
         cur.ld = ld;
+        cur.id = __builtin_amdgcn_readfirstlane(tab_id[bl]);
         break;
       }
     }
@@ -562,12 +677,6 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   // (rather than every step) halves the time waves spend waiting for the
   // slowest one; the MFMAs issued before it keep the matrix pipe busy
   // meanwhile.  Vector-memory loads complete in issue order.
-  int ntiles = 0;
-  for (int bl = 0; bl < n_docs; ++bl) {
-    int s0;
-    int ld;
-    if (doc_ok(bl, s0, ld)) ntiles += (ld + kTileRows - 1) / kTileRows;
-  }
   if (ntiles == 0) return;
 
   constexpr int kNB = kTileBuffers;
@@ -719,8 +828,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
         const float sm = half_sum(vtok ? m[j] : 0.0f);
         part_sum = (part == 0) ? sm : part_sum + sm;
         if ((j < a.qpw * a.nblk) && (q < a.nq)) {
-          if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + b_begin + cur.b) * a.lq + tok] = am[j];
-          if (part == a.nblk - 1 && lane == kHalfSumLane) scores[q * a.nb + b_begin + cur.b] = part_sum;
+          if (ARGMAX && argmax_out && h == 0 && vtok) argmax_out[(q * a.nb + cur.id) * a.lq + tok] = am[j];
+          if (part == a.nblk - 1 && lane == kHalfSumLane) scores[q * a.nb + cur.id] = part_sum;
         }
         m[j] = -__builtin_inff();
         am[j] = 0;
@@ -1052,7 +1161,7 @@ constexpr int kDocGroupThreads = 1024;
 // documents of one length over four counters (C4's lengths fall into a few
 // tile counts, and same-address LDS atomics serialise)
 constexpr int kLenClasses = 256;
-constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 9 bytes per document
+constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 5 bytes per document
 
 // A chunk: the document's rows and, per pair slot, its pair, resolved by
 // scatter_docs_kernel; doc_chunk_kernel copies its chunks into LDS.
@@ -1093,100 +1202,154 @@ __device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p)
 // out in coalesced passes: a single CU writing scattered words is what costs
 // here (about one cache line per clock), so the scattered writes -- the
 // chunk records -- are left to scatter_docs_kernel, which spreads them over
-// the chip.  The ids and offsets are loaded up front, in independent
-// batches: a one-workgroup kernel takes as long as its chain of dependent
-// round trips.  A pair whose document id is out of range is written off
-// here (NaN score, zero argmax row).  Chunk positions within a class follow
-// the atomics; no result depends on them.
-constexpr int kGroupPairBatch = 24;  // pair ids per thread per batch
-constexpr int kGroupDocBatch = 8;    // document extents per thread per batch
+// the chip.  A one-workgroup kernel takes as long as its chain of dependent
+// round trips and the instructions its one CU issues, so the pair ids and
+// document offsets are loaded up front, 16 bytes per lane where aligned
+// (VEC), and a thread owns four consecutive pairs per vector and eight
+// consecutive documents.  A pair whose document id is out of range is
+// written off here (NaN score, zero argmax row).  Chunk positions within a
+// class follow the atomics; no result depends on them.
+constexpr int kGroupPairVecs = 5;  // 4-pair vectors per thread per batch (20,480 pairs)
+constexpr int kGroupDocs = 8;      // consecutive documents per thread
+
+// v[0..3] = p[i0 .. i0 + 3], zero past n (one 16-byte load where VEC and
+// whole; p + i0 is then 16-byte aligned since i0 % 4 == 0)
+template <bool VEC>
+__device__ __forceinline__ void load4_bounded(const int32_t* __restrict__ p, int64_t i0, int64_t n,
+                                              int32_t (&v)[4]) {
+  if (VEC && i0 + 3 < n) {
+    const int4 x = *reinterpret_cast<const int4*>(p + i0);
+    v[0] = x.x;
+    v[1] = x.y;
+    v[2] = x.z;
+    v[3] = x.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = i0 + e < n ? p[i0 + e] : 0;
+  }
+}
+
+// p[d0 .. d0 + 7] = v[0..7] for the entries below n (two 16-byte stores when
+// p is 16-byte aligned and all eight are in range)
+__device__ __forceinline__ void store8_bounded(int32_t* __restrict__ p, int d0, int n,
+                                               const int32_t (&v)[kGroupDocs]) {
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0 && d0 + 7 < n) {
+    *reinterpret_cast<int4*>(p + d0) = int4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<int4*>(p + d0 + 4) = int4{v[4], v[5], v[6], v[7]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < kGroupDocs; ++e)
+      if (d0 + e < n) p[d0 + e] = v[e];
+  }
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a, DocChunks g) {
-  extern __shared__ int32_t cnt[];            // [nd] pairs per document
+  extern __shared__ int32_t cnt[];            // [nd8] pairs per document, zero past nd
   __shared__ int32_t cls[kLenClasses];        // chunks per class, then cursors
   static_assert(kLenClasses == 4 * 64, "four classes per lane of wave 0");
-  constexpr int UP = kGroupPairBatch, UD = kGroupDocBatch;
+  constexpr int T = kDocGroupThreads, UV = kGroupPairVecs, ND = kGroupDocs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nd = (int)a.nd;
+  const int nd8 = (nd + ND - 1) & ~(ND - 1);
   const int64_t np = a.npairs;
-  int32_t* cpos = cnt + nd;                                // [nd] first chunk
-  uint8_t* kls = reinterpret_cast<uint8_t*>(cpos + nd);    // [nd] length class
+  uint8_t* kls = reinterpret_cast<uint8_t*>(cnt + nd8);  // [nd8] length class
 
-  // the first UP pair ids and UD document extents of this thread, loaded
-  // before anything waits on them
-  int32_t di[UP];
+  // the first batch of pair ids and this thread's first eight document
+  // extents, loaded before anything waits on them
+  int32_t di[UV][4];
+  auto load_pairs = [&](int64_t v0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int u = 0; u < UP; ++u) {
-    const int64_t p = tid + (int64_t)u * kDocGroupThreads;
-    di[u] = p < np ? a.dids[p] : 0;
-  }
-  int32_t o_lo[UD], o_hi[UD];
+    for (int u = 0; u < UV; ++u) load4_bounded<VEC>(a.dids, 4 * (v0 + (int64_t)u * T), np, di[u]);
+  };
+  int32_t off[ND + 1];
+  auto load_docs = [&](int d0) __attribute__((always_inline)) {
+    int32_t lo[4], hi[4];
+    load4_bounded<VEC>(a.doff, d0, (int64_t)nd + 1, lo);
+    load4_bounded<VEC>(a.doff, d0 + 4, (int64_t)nd + 1, hi);
 #pragma unroll
-  for (int u = 0; u < UD; ++u) {
-    const int d = tid + u * kDocGroupThreads;
-    o_lo[u] = d < nd ? a.doff[d] : 0;
-    o_hi[u] = d < nd ? a.doff[d + 1] : 0;
-  }
-  for (int d = tid; d < nd; d += kDocGroupThreads) cnt[d] = 0;
+    for (int e = 0; e < 4; ++e) {
+      off[e] = lo[e];
+      off[4 + e] = hi[e];
+    }
+    off[ND] = d0 + ND <= nd ? a.doff[d0 + ND] : 0;
+  };
+  load_pairs(tid);
+  load_docs(ND * tid);
+  for (int d = tid; d < nd8; d += T) cnt[d] = 0;
   if (tid < kLenClasses) cls[tid] = 0;
-  __syncthreads();
+  // a barrier that waits for this thread's LDS writes only: the loads above
+  // are waited for where they are used
+  auto lds_barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+  };
+  lds_barrier();
 
   // 1. pairs per document; a batch holding an out-of-range document id
   //    writes its pairs off in a second, rolled loop (rare)
-  auto count_batch = [&](int64_t p0) __attribute__((always_inline)) {
+  auto count_batch = [&](int64_t v0) __attribute__((always_inline)) {
     bool bad = false;
 #pragma unroll
-    for (int u = 0; u < UP; ++u) {
-      const bool in = p0 + (int64_t)u * kDocGroupThreads < np;
-      if (in && di[u] >= 0 && di[u] < nd)
-        atomicAdd(&cnt[di[u]], 1);
-      else
-        bad |= in;
-    }
+    for (int u = 0; u < UV; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = 4 * (v0 + (int64_t)u * T) + e < np;
+        const int32_t d = di[u][e];
+        if (in && d >= 0 && d < nd)
+          atomicAdd(&cnt[d], 1);
+        else
+          bad |= in;
+      }
     if (bad) {
 #pragma unroll 1
-      for (int u = 0; u < UP; ++u) {
-        const int64_t p = p0 + (int64_t)u * kDocGroupThreads;
-        if (p >= np) break;
-        const int32_t d = a.dids[p];
-        if (d < 0 || d >= nd) write_unrouted_pair(a, p);
-      }
+      for (int u = 0; u < UV; ++u)
+#pragma unroll 1
+        for (int e = 0; e < 4; ++e) {
+          const int64_t p = 4 * (v0 + (int64_t)u * T) + e;
+          if (p >= np) break;
+          const int32_t d = a.dids[p];
+          if (d < 0 || d >= nd) write_unrouted_pair(a, p);
+        }
     }
   };
+  const int64_t nv = (np + 3) / 4;
   count_batch(tid);
-  for (int64_t p0 = tid + (int64_t)UP * kDocGroupThreads; p0 < np;
-       p0 += (int64_t)UP * kDocGroupThreads) {
-#pragma unroll
-    for (int u = 0; u < UP; ++u) {
-      const int64_t p = p0 + (int64_t)u * kDocGroupThreads;
-      di[u] = p < np ? a.dids[p] : 0;
-    }
-    count_batch(p0);
+  for (int64_t v0 = tid + (int64_t)UV * T; v0 < nv; v0 += (int64_t)UV * T) {
+    load_pairs(v0);
+    count_batch(v0);
   }
-  __syncthreads();
+  lds_barrier();
 
   // 2. length class of every document, and the chunks of each class
-  auto classify = [&](int d, int32_t lo_off, int32_t hi_off) __attribute__((always_inline)) {
-    if (d >= nd) return;
-    const int64_t ld = (int64_t)hi_off - lo_off;
-    const int64_t t = ld <= 0 ? 0 : (ld + kTileRows - 1) / kTileRows;
-    const int k = 4 * (63 - (int)(t < 63 ? t : 63)) + (d & 3);
-    kls[d] = (uint8_t)k;
-    const int c = cnt[d];
-    if (c > 0) atomicAdd(&cls[k], (c + kChunkPairs - 1) / kChunkPairs);
-  };
+  auto classify = [&](int d0) __attribute__((always_inline)) {
+    if (d0 >= nd) return;
+    const int4 c_lo = *reinterpret_cast<const int4*>(cnt + d0);
+    const int4 c_hi = *reinterpret_cast<const int4*>(cnt + d0 + 4);
+    const int32_t c8[ND] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
+    uint32_t k_lo = 0, k_hi = 0;
 #pragma unroll
-  for (int u = 0; u < UD; ++u) classify(tid + u * kDocGroupThreads, o_lo[u], o_hi[u]);
-  for (int d0 = tid + UD * kDocGroupThreads; d0 < nd; d0 += UD * kDocGroupThreads) {
-#pragma unroll
-    for (int u = 0; u < UD; ++u) {
-      const int d = d0 + u * kDocGroupThreads;
-      o_lo[u] = d < nd ? a.doff[d] : 0;
-      o_hi[u] = d < nd ? a.doff[d + 1] : 0;
+    for (int e = 0; e < ND; ++e) {
+      const int d = d0 + e;
+      const int64_t ld = (int64_t)off[e + 1] - off[e];
+      const int64_t t = ld <= 0 ? 0 : (ld + kTileRows - 1) / kTileRows;
+      const int k = 4 * (63 - (int)(t < 63 ? t : 63)) + (d & 3);
+      if (e < 4)
+        k_lo |= (uint32_t)k << (8 * e);
+      else
+        k_hi |= (uint32_t)k << (8 * (e - 4));
+      if (d < nd && c8[e] > 0) atomicAdd(&cls[k], (c8[e] + kChunkPairs - 1) / kChunkPairs);
     }
-#pragma unroll
-    for (int u = 0; u < UD; ++u) classify(d0 + u * kDocGroupThreads, o_lo[u], o_hi[u]);
+    *reinterpret_cast<uint2*>(kls + d0) = uint2{k_lo, k_hi};
+  };
+  classify(ND * tid);
+  for (int d0 = ND * (tid + T); d0 < nd; d0 += ND * T) {
+    load_docs(d0);
+    classify(d0);
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. exclusive scan of the class counts (wave 0, four classes per lane)
   if (wave == 0) {
@@ -1199,9 +1362,9 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
     }
     int ci = run;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int u = __shfl_up(ci, off);
-      if (lane >= off) ci += u;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(ci, o);
+      if (lane >= o) ci += u;
     }
     int first = ci - run;
 #pragma unroll
@@ -1211,14 +1374,26 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
     }
     if (lane == 63) g.nchunks[0] = ci;
   }
-  __syncthreads();
+  lds_barrier();
 
   // 4. each document's first chunk, and the coalesced copy-out
-  for (int d = tid; d < nd; d += kDocGroupThreads) {
-    const int c = cnt[d];
-    g.cnt[d] = c;
-    g.dcur[d] = 0;
-    g.cpos[d] = c > 0 ? atomicAdd(&cls[kls[d]], (c + kChunkPairs - 1) / kChunkPairs) : 0;
+  const int32_t zero8[ND] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int d0 = ND * tid; d0 < nd; d0 += ND * T) {
+    const int4 c_lo = *reinterpret_cast<const int4*>(cnt + d0);
+    const int4 c_hi = *reinterpret_cast<const int4*>(cnt + d0 + 4);
+    const int32_t c8[ND] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
+    const uint2 kk = *reinterpret_cast<const uint2*>(kls + d0);
+    int32_t p8[ND];
+#pragma unroll
+    for (int e = 0; e < ND; ++e) {
+      const int k = (int)(((e < 4 ? kk.x : kk.y) >> (8 * (e & 3))) & 0xFFu);
+      p8[e] = d0 + e < nd && c8[e] > 0
+                  ? atomicAdd(&cls[k], (c8[e] + kChunkPairs - 1) / kChunkPairs)
+                  : 0;
+    }
+    store8_bounded(g.cnt, d0, nd, c8);
+    store8_bounded(g.dcur, d0, nd, zero8);
+    store8_bounded(g.cpos, d0, nd, p8);
   }
 }
 
@@ -1299,10 +1474,14 @@ struct ChunkOcc {
 };
 
 // Chunk of round r for workgroup b of `grid`: the sorted chunks are dealt
-// in snake order (b, then grid - 1 - b, ...) so that no workgroup takes the
-// largest chunk of every round.
+// in snake order (place q, then grid - 1 - q, ...) so that no workgroup takes
+// the largest chunk of every round.  With a grid of whole XCD rows the
+// places of a round are dealt XCD by XCD (place q to workgroup
+// (q % (grid / 8)) * 8 + q / (grid / 8)): the chunks of one document are
+// consecutive, so they run at once on one XCD and share its L2.
 __device__ __forceinline__ int64_t snake_chunk(int b, int r, int grid) {
-  return (int64_t)r * grid + ((r & 1) ? grid - 1 - b : b);
+  const int q = grid % kXcds == 0 ? (b % kXcds) * (grid / kXcds) + b / kXcds : b;
+  return (int64_t)r * grid + ((r & 1) ? grid - 1 - q : q);
 }
 
 // s_waitcnt vmcnt(N) (N <= 63); encoding (gfx9): vmcnt[3:0] | expcnt[6:4]
@@ -1712,7 +1891,7 @@ static size_t doc_chunk_ws_bytes(int64_t nd, int64_t npairs) {
 }
 
 // Grid: as many workgroups as the chip holds at once (LDS or registers
-// bound it: three per CU at dim 128), so the chunks are dealt in one round;
+// bound it: two per CU at dim 128), so the chunks are dealt in one round;
 // more only where one workgroup would otherwise get over kChunkBatch.
 template <typename T, int KS, bool ARGMAX>
 static int launch_doc_chunk_v(const FwdArgs& a, const DocChunks& g, int64_t bound,
@@ -1753,14 +1932,19 @@ static int run_doc_chunks(const FwdArgs& a, maxsim_dtype dtype, void* workspace,
   g.cnt = g.nchunks + 4;
   g.dcur = g.cnt + a.nd;
   g.cpos = g.dcur + a.nd;
-  // one workgroup counts and scans (9 bytes of LDS per document) ...
-  const size_t glds = (size_t)a.nd * (2 * sizeof(int32_t) + 1);
+  // one workgroup counts and scans (5 bytes of LDS per document) ...
+  const size_t glds = (size_t)((a.nd + kGroupDocs - 1) / kGroupDocs * kGroupDocs) *
+                      (sizeof(int32_t) + 1);
+  const bool vec = aligned16(a.dids) && aligned16(a.doff);
+  const auto gkern = vec ? group_docs_kernel<true> : group_docs_kernel<false>;
   if (glds > 64 * 1024) {
-    static std::atomic<bool> raised[kMaxDevices];
-    if (int e = raise_lds_limit((const void*)group_docs_kernel, glds, "group_docs_kernel", raised))
+    // once per device, to what the largest grouping needs
+    static std::atomic<bool> raised[2][kMaxDevices];
+    if (int e = raise_lds_limit((const void*)gkern, (size_t)kDocGroupMaxDocs * (sizeof(int32_t) + 1),
+                                "group_docs_kernel", raised[vec]))
       return e;
   }
-  hipLaunchKernelGGL(group_docs_kernel, dim3(1), dim3(kDocGroupThreads), glds, st, a, g);
+  hipLaunchKernelGGL(gkern, dim3(1), dim3(kDocGroupThreads), glds, st, a, g);
   // ... and the chip scatters the pair ids and the chunk table
   const int64_t n = std::max<int64_t>(a.npairs, a.nd);
   const int64_t sgrid = std::min<int64_t>((n + 255) / 256, 4 * (int64_t)device_cus());
@@ -1824,7 +2008,7 @@ constexpr int tiled_nbw() {
 
 template <typename T, int KS>
 static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
-  if constexpr (4 * 32 * KS * 16 * T::bytes + 4 * (kMaxDocsPerGroup + 1) > 64 * 1024) {
+  if constexpr (4 * 32 * KS * 16 * T::bytes + kDocTableBytes > 64 * 1024) {
     return;  // excluded by tiled_supported(): four buffers would exceed 64 KB
   } else {
   constexpr int NBW = tiled_nbw<T, KS>();
@@ -1847,8 +2031,7 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
   const int64_t total = (int64_t)a.n_qg * a.n_dc;
   const int64_t per_xcd = (total + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8));
-  const size_t lds = kTileBuffers * G::kBufPieces * sizeof(uint4) +
-                     (kMaxDocsPerGroup + 1) * sizeof(int);
+  const size_t lds = kTileBuffers * G::kBufPieces * sizeof(uint4) + kDocTableBytes;
   // Score-only calls use the same kernel with argmax == nullptr: a variant
   // without the index search needs more registers under this schedule and
   // spills, which costs far more than the search.
@@ -1860,9 +2043,9 @@ static void launch_tiled_ks(TiledArgs a, hipStream_t st) {
 template <typename T>
 static bool tiled_supported(int dim, int lq) {
   const int ks = ks_for_dim(dim);
-  // four LDS tile buffers of 32 rows x ks*16 elements (plus the offset
-  // table) must fit in 64 KB
-  if (4 * 32 * ks * 16 * T::bytes + 4 * (kMaxDocsPerGroup + 1) > 64 * 1024) return false;
+  // four LDS tile buffers of 32 rows x ks*16 elements (plus the document
+  // list) must fit in 64 KB
+  if (4 * 32 * ks * 16 * T::bytes + kDocTableBytes > 64 * 1024) return false;
   int nbw = 1;
   switch (ks) {
     case 2: nbw = tiled_nbw<T, 2>(); break;

@@ -313,6 +313,59 @@ def test_contrastive_work_balanced_chunks(nb, lo, hi):
     _check_forward(q, d, off, scores, argmax)
 
 
+@pytest.mark.parametrize("nq,nb,lo,hi,n_long", [
+    (64, 300, 1, 1500, 0), (1, 511, 1, 700, 0), (16, 512, 100, 1100, 5), (64, 65, 1, 40, 0)],
+    ids=["64q-300-skewed", "1q-511", "16q-512-long", "64q-65-short"])
+def test_contrastive_dealt_chunks(nq, nb, lo, hi, n_long):
+    """At most 512 documents and more chunks than one: the documents are
+    ranked by tile count on the device (every workgroup the same ranks;
+    counts past 127 tiles share one key, ties by index) and dealt to the
+    chunks in snake order.  Every (query, document) score comes from exactly
+    one workgroup: checked against the oracle, with documents longer than
+    127 tiles and documents of one row."""
+    gen = torch.Generator().manual_seed(nb * 7 + nq)
+    lens = torch.randint(lo, hi + 1, (nb,), generator=gen)
+    lens[torch.randperm(nb, generator=gen)[:n_long]] = torch.randint(4100, 6000, (n_long,),
+                                                                      generator=gen)
+    lens[nb // 2] = 1
+    q, d, off = make_contrastive(nq, 32, 128, lens.tolist(), torch.bfloat16, seed=nb + 5,
+                                 unit=True)
+    scores, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    _check_forward(q, d, off, scores, argmax)
+    assert torch.equal(maxsim_amd.score_contrastive(q, d, off), scores)
+
+
+def test_contrastive_dealt_chunks_invalid_offsets_at_the_operator_level():
+    """The dealt chunks with offsets that decrease at a few documents (called
+    past the Python checks): those documents rank last (no tiles), get a NaN
+    score and argmax 0; the others their MaxSim."""
+    nb = 300
+    gen = torch.Generator().manual_seed(5)
+    lens = torch.randint(20, 400, (nb,), generator=gen)
+    q, d, off = make_contrastive(64, 32, 64, lens.tolist(), torch.bfloat16, seed=9, unit=True)
+    off = off.clone()
+    bad_docs = [10, 11, 150]
+    off_h = off.cpu()
+    for b in bad_docs:
+        off_h[b + 1] = off_h[b] - 1          # end before start: document b invalid
+    off = off_h.to(DEVICE)
+    scores, argmax = ops.maxsim_contrastive_forward_with_argmax(q, d, off)
+    invalid = set()
+    on = npi(off)
+    for b in range(nb):
+        if not (on[b] >= 0 and on[b + 1] > on[b] and on[b + 1] <= d.shape[0]):
+            invalid.add(b)
+    assert invalid >= set(bad_docs)
+    bad = torch.tensor(sorted(invalid), device=DEVICE)
+    assert torch.isnan(scores[:, bad]).all() and torch.all(argmax[:, bad] == 0)
+    good = [b for b in range(nb) if b not in invalid]
+    qn, dn = np64(q), np64(d)
+    for b in good[::37]:
+        s_ref, _ = oracle.contrastive_forward(qn, dn[on[b]:on[b + 1]],
+                                              np.array([0, on[b + 1] - on[b]], dtype=np.int64))
+        assert_close(scores[:, b:b + 1], s_ref, **SCORE_TOL[torch.bfloat16])
+
+
 def test_contrastive_malformed_offsets_at_the_operator_level():
     """Offsets that decrease (the Python layer rejects them; the operator is
     called directly): documents with an invalid range get a NaN score and

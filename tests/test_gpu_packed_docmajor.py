@@ -5,7 +5,8 @@ the same inputs, bit for bit, and against the oracle.  The torch ops pass a
 workspace; a max_q_len of 65 selects pair_kernel on the same pairs.  Cases
 the grouping must route: pairs with an out-of-range query or document id,
 empty document segments, a document named by hundreds of pairs (many
-chunks of four), documents named by no pair, and both query block counts."""
+chunks of four), documents named by no pair, both query block counts, and
+sparse pairs (partly filled chunks)."""
 
 from __future__ import annotations
 
@@ -82,6 +83,43 @@ def test_doc_major_repeatable_and_order_free():
     s3, a3 = ops.maxsim_packed_forward_with_argmax(q, qo, d, do, qi[perm], di[perm], 64)
     torch.testing.assert_close(s3, s1[perm], rtol=0, atol=0, equal_nan=True)
     assert torch.equal(a3, a1[perm])
+
+
+@pytest.mark.parametrize("qlen", [(1, 65), (33, 65)], ids=["mixed_blocks", "two_blocks"])
+@pytest.mark.parametrize("seed,shift", [(0, 0), (1, 1)], ids=["aligned", "ids_offsets_unaligned"])
+def test_doc_major_sparse_pairs(qlen, seed, shift):
+    """C4-like sparsity (about 2.3 pairs per document): most chunks are
+    partly filled (empty pair slots), with one or two query blocks per pair;
+    documents whose pairs all name invalid queries give chunks with no tile
+    among the others.  With shift 1 the document ids and offsets start 4
+    bytes past a 16-byte boundary (the grouping's element-wise loads)."""
+    gen = torch.Generator().manual_seed(100 + seed)
+    nq, nd, npairs, dim = 61, 3000, 7000, 128
+    ql = torch.randint(qlen[0], qlen[1], (nq,), generator=gen)
+    dl = torch.randint(1, 400, (nd,), generator=gen)
+    q = torch.randn(int(ql.sum()), dim, generator=gen).to(torch.bfloat16)
+    d = torch.randn(int(dl.sum()), dim, generator=gen).to(torch.bfloat16)
+    qids = torch.randint(0, nq, (npairs,), generator=gen, dtype=torch.int32)
+    dids = torch.randint(0, nd, (npairs,), generator=gen, dtype=torch.int32)
+    dead = torch.arange(7, nd, 97)       # documents named only by invalid queries
+    qids[torch.isin(dids, dead)] = nq
+    bad = torch.isin(dids, dead)
+    def shifted(t):
+        return torch.cat([t.new_zeros(shift), t]).to(DEVICE)[shift:]
+    q, qo, d = q.to(DEVICE), offsets_from_lengths(ql).to(DEVICE), d.to(DEVICE)
+    do, qi, di = shifted(offsets_from_lengths(dl)), qids.to(DEVICE), shifted(dids)
+    assert (di.data_ptr() % 16 == 0) == (shift == 0) and (do.data_ptr() % 16 == 0) == (shift == 0)
+    s_doc, a_doc = ops.maxsim_packed_forward_with_argmax(q, qo, d, do, qi, di, 64)
+    s_pair, a_pair = ops.maxsim_packed_forward_with_argmax(q, qo, d, do, qi, di, 65)
+    torch.testing.assert_close(s_doc, s_pair, rtol=0, atol=0, equal_nan=True)
+    assert torch.equal(a_doc, a_pair[:, :64])
+    badd = bad.to(DEVICE)
+    assert torch.all(torch.isnan(s_doc[badd])) and torch.all(a_doc[badd] == 0)
+    assert not torch.any(torch.isnan(s_doc[~badd]))
+    ok = ~badd
+    qn, dn, qon, don = np64(q), np64(d), npi(qo), npi(do)
+    s_ref, _ = oracle.packed_forward(qn, qon, dn, don, npi(qi[ok]), npi(di[ok]), 64)
+    assert_close(s_doc[ok], s_ref, **SCORE_TOL[torch.bfloat16])
 
 
 def test_c_abi_workspace_fallbacks():
