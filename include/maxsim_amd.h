@@ -92,8 +92,9 @@ int maxsim_amd_packed_forward_with_argmax(
     int64_t max_q_len, float* scores, int32_t* argmax, void* stream);
 
 /* Bytes of device workspace that let maxsim_amd_packed_forward_with_argmax_ws
- * score the pairs document by document: 64 * (ceil(num_pairs / 4) +
- * min(num_documents, num_pairs)) + 16 + 12 * num_documents.  No counterpart
+ * score the pairs document by document: R + 16384 + num_documents, where R
+ * is 64 * (ceil(num_pairs / 4) + min(num_documents, num_pairs)) + 16 +
+ * 12 * num_documents rounded up to a multiple of 16.  No counterpart
  * in the reference, whose packed forward scores the pairs in the caller's
  * order. */
 size_t maxsim_amd_packed_forward_workspace_size(int64_t num_documents, int64_t num_pairs);

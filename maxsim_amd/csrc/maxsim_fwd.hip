@@ -1161,7 +1161,7 @@ constexpr int kDocGroupThreads = 1024;
 // documents of one length over four counters (C4's lengths fall into a few
 // tile counts, and same-address LDS atomics serialise)
 constexpr int kLenClasses = 256;
-constexpr int64_t kDocGroupMaxDocs = 16384;   // LDS: 5 bytes per document
+constexpr int64_t kDocGroupMaxDocs = 16384;   // 1024 per grouping workgroup
 
 // A chunk: the document's rows and, per pair slot, its pair, resolved by
 // scatter_docs_kernel; doc_chunk_kernel copies its chunks into LDS.
@@ -1175,12 +1175,16 @@ struct ChunkMeta {
 };
 static_assert(sizeof(ChunkMeta) % 16 == 0, "chunks are copied as 16-byte pieces");
 
+// The grouping's workspace (see doc_chunk_ws_bytes for the layout).
+constexpr int kGroupWgs = 16;  // grouping workgroups, one range of documents each
 struct DocChunks {
   ChunkMeta* recs;   // [max chunks], sorted by their document's length class
   int32_t* nchunks;  // [1]
   int32_t* cnt;      // [nd] pairs per document
   int32_t* dcur;     // [nd] pairs of each document placed so far
-  int32_t* cpos;     // [nd] each document's first chunk
+  int32_t* cpos;     // [nd] each document's first chunk within (range, class)
+  int32_t* hist;     // [kGroupWgs][kLenClasses] chunks per (range, class)
+  uint8_t* kls;      // [nd] length class
 };
 
 // Upper bound on the chunks of a grouping: ceil(c / 4) <= c / 4 + 3 / 4 per
@@ -1189,6 +1193,14 @@ static int64_t doc_chunk_bound(int64_t nd, int64_t npairs) {
   return (npairs + kChunkPairs - 1) / kChunkPairs + std::min(nd, npairs);
 }
 
+// Documents per grouping range: a multiple of eight, kGroupWgs ranges cover
+// all (at most 1024 each since nd <= kDocGroupMaxDocs).
+__host__ __device__ __forceinline__ int group_range(int nd) {
+  return ((nd + kGroupWgs - 1) / kGroupWgs + 7) & ~7;
+}
+static_assert(((kDocGroupMaxDocs + kGroupWgs - 1) / kGroupWgs + 7) / 8 * 8 <= 1024,
+              "a range fits one batch of eight documents per thread");
+
 // NaN score and zero argmax row for a pair no chunk carries (one thread).
 __device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p) {
   a.scores[p] = __builtin_nanf("");
@@ -1196,19 +1208,19 @@ __device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p)
     for (int t = 0; t < a.slots; ++t) a.argmax[p * a.slots + t] = 0;
 }
 
-// group_docs_kernel (one workgroup): pairs per document (LDS counters),
-// each document's length class (LDS bytes), and each document's first chunk
-// by a counting sort over the length classes (LDS cursors).  Its outputs go
-// out in coalesced passes: a single CU writing scattered words is what costs
-// here (about one cache line per clock), so the scattered writes -- the
-// chunk records -- are left to scatter_docs_kernel, which spreads them over
-// the chip.  A one-workgroup kernel takes as long as its chain of dependent
-// round trips and the instructions its one CU issues, so the pair ids and
-// document offsets are loaded up front, 16 bytes per lane where aligned
-// (VEC), and a thread owns four consecutive pairs per vector and eight
-// consecutive documents.  A pair whose document id is out of range is
-// written off here (NaN score, zero argmax row).  Chunk positions within a
-// class follow the atomics; no result depends on them.
+// group_docs_kernel (kGroupWgs workgroups): workgroup k owns the documents
+// of range k.  It reads every pair id and counts the pairs of its range in
+// LDS counters, classifies its documents (length class, chunks per class),
+// writes its chunks per class to hist[k], and gives each of its documents
+// a first chunk within (range, class) by LDS cursors.  scatter_docs_kernel
+// turns those into global positions (classes in order, ranges in order
+// within a class).  A one-workgroup version took 11.3 us at C4: its time was
+// its CU's chain of LDS atomics and round trips.  The ids and offsets are
+// loaded up front, 16 bytes per lane where aligned (VEC); a thread owns four
+// consecutive pairs per vector and eight consecutive documents.  Pairs whose
+// document id is out of range are written off by workgroup 0 (NaN score,
+// zero argmax row).  Chunk positions within a (range, class) follow the
+// atomics; no result depends on them.
 constexpr int kGroupPairVecs = 5;  // 4-pair vectors per thread per batch (20,480 pairs)
 constexpr int kGroupDocs = 8;      // consecutive documents per thread
 
@@ -1245,39 +1257,45 @@ __device__ __forceinline__ void store8_bounded(int32_t* __restrict__ p, int d0, 
 
 template <bool VEC>
 __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a, DocChunks g) {
-  extern __shared__ int32_t cnt[];            // [nd8] pairs per document, zero past nd
-  __shared__ int32_t cls[kLenClasses];        // chunks per class, then cursors
-  static_assert(kLenClasses == 4 * 64, "four classes per lane of wave 0");
+  __shared__ int32_t cnt[1024];               // pairs per document of the range
+  __shared__ int32_t cls[kLenClasses];        // chunks per class
+  __shared__ int32_t cur[kLenClasses];        // cursors per class
   constexpr int T = kDocGroupThreads, UV = kGroupPairVecs, ND = kGroupDocs;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int nd = (int)a.nd;
-  const int nd8 = (nd + ND - 1) & ~(ND - 1);
+  const int per = group_range(nd);
+  const int d_lo = min((int)blockIdx.x * per, nd);
+  const int d_hi = min(d_lo + per, nd);
   const int64_t np = a.npairs;
-  uint8_t* kls = reinterpret_cast<uint8_t*>(cnt + nd8);  // [nd8] length class
+  const bool writer = blockIdx.x == 0;  // writes off the pairs of invalid documents
 
-  // the first batch of pair ids and this thread's first eight document
-  // extents, loaded before anything waits on them
+  // the first batch of pair ids and this thread's eight document extents,
+  // loaded before anything waits on them
   int32_t di[UV][4];
   auto load_pairs = [&](int64_t v0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < UV; ++u) load4_bounded<VEC>(a.dids, 4 * (v0 + (int64_t)u * T), np, di[u]);
   };
+  const int d0 = d_lo + ND * tid;  // this thread's documents: d0 .. d0 + 7 (below d_hi)
   int32_t off[ND + 1];
-  auto load_docs = [&](int d0) __attribute__((always_inline)) {
+  {
     int32_t lo[4], hi[4];
-    load4_bounded<VEC>(a.doff, d0, (int64_t)nd + 1, lo);
-    load4_bounded<VEC>(a.doff, d0 + 4, (int64_t)nd + 1, hi);
+    const int64_t lim = d0 < d_hi ? (int64_t)nd + 1 : 0;
+    load4_bounded<VEC>(a.doff, d0, lim, lo);
+    load4_bounded<VEC>(a.doff, d0 + 4, lim, hi);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       off[e] = lo[e];
       off[4 + e] = hi[e];
     }
-    off[ND] = d0 + ND <= nd ? a.doff[d0 + ND] : 0;
-  };
+    off[ND] = d0 < d_hi && d0 + ND <= nd ? a.doff[d0 + ND] : 0;
+  }
   load_pairs(tid);
-  load_docs(ND * tid);
-  for (int d = tid; d < nd8; d += T) cnt[d] = 0;
-  if (tid < kLenClasses) cls[tid] = 0;
+  cnt[tid] = 0;
+  if (tid < kLenClasses) {
+    cls[tid] = 0;
+    cur[tid] = 0;
+  }
   // a barrier that waits for this thread's LDS writes only: the loads above
   // are waited for where they are used
   auto lds_barrier = [&]() __attribute__((always_inline)) {
@@ -1288,8 +1306,8 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
   };
   lds_barrier();
 
-  // 1. pairs per document; a batch holding an out-of-range document id
-  //    writes its pairs off in a second, rolled loop (rare)
+  // 1. pairs per document of the range; workgroup 0 writes off, in a second,
+  //    rolled loop (rare), the pairs of a batch holding an out-of-range id
   auto count_batch = [&](int64_t v0) __attribute__((always_inline)) {
     bool bad = false;
 #pragma unroll
@@ -1298,12 +1316,10 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
       for (int e = 0; e < 4; ++e) {
         const bool in = 4 * (v0 + (int64_t)u * T) + e < np;
         const int32_t d = di[u][e];
-        if (in && d >= 0 && d < nd)
-          atomicAdd(&cnt[d], 1);
-        else
-          bad |= in;
+        if (in && d >= d_lo && d < d_hi) atomicAdd(&cnt[d - d_lo], 1);
+        bad |= in && (d < 0 || d >= nd);
       }
-    if (bad) {
+    if (writer && bad) {
 #pragma unroll 1
       for (int u = 0; u < UV; ++u)
 #pragma unroll 1
@@ -1323,103 +1339,112 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
   }
   lds_barrier();
 
-  // 2. length class of every document, and the chunks of each class
-  auto classify = [&](int d0) __attribute__((always_inline)) {
-    if (d0 >= nd) return;
-    const int4 c_lo = *reinterpret_cast<const int4*>(cnt + d0);
-    const int4 c_hi = *reinterpret_cast<const int4*>(cnt + d0 + 4);
-    const int32_t c8[ND] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
-    uint32_t k_lo = 0, k_hi = 0;
+  // 2. length class of every document of the range, and chunks per class
+  int32_t c8[ND];
+  int32_t k8[ND];
+  const bool mine = d0 < d_hi;
+  if (mine) {
 #pragma unroll
     for (int e = 0; e < ND; ++e) {
       const int d = d0 + e;
       const int64_t ld = (int64_t)off[e + 1] - off[e];
       const int64_t t = ld <= 0 ? 0 : (ld + kTileRows - 1) / kTileRows;
-      const int k = 4 * (63 - (int)(t < 63 ? t : 63)) + (d & 3);
-      if (e < 4)
-        k_lo |= (uint32_t)k << (8 * e);
-      else
-        k_hi |= (uint32_t)k << (8 * (e - 4));
-      if (d < nd && c8[e] > 0) atomicAdd(&cls[k], (c8[e] + kChunkPairs - 1) / kChunkPairs);
+      k8[e] = 4 * (63 - (int)(t < 63 ? t : 63)) + (d & 3);
+      c8[e] = d < d_hi ? cnt[d - d_lo] : 0;
+      if (c8[e] > 0) atomicAdd(&cls[k8[e]], (c8[e] + kChunkPairs - 1) / kChunkPairs);
     }
-    *reinterpret_cast<uint2*>(kls + d0) = uint2{k_lo, k_hi};
-  };
-  classify(ND * tid);
-  for (int d0 = ND * (tid + T); d0 < nd; d0 += ND * T) {
-    load_docs(d0);
-    classify(d0);
   }
   lds_barrier();
+  if (tid < kLenClasses) g.hist[blockIdx.x * kLenClasses + tid] = cls[tid];
 
-  // 3. exclusive scan of the class counts (wave 0, four classes per lane)
-  if (wave == 0) {
-    int c4[4];
-    int run = 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      c4[u] = cls[4 * lane + u];
-      run += c4[u];
-    }
-    int ci = run;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(ci, o);
-      if (lane >= o) ci += u;
-    }
-    int first = ci - run;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      cls[4 * lane + u] = first;  // first chunk of the class
-      first += c4[u];
-    }
-    if (lane == 63) g.nchunks[0] = ci;
-  }
-  lds_barrier();
-
-  // 4. each document's first chunk, and the coalesced copy-out
-  const int32_t zero8[ND] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int d0 = ND * tid; d0 < nd; d0 += ND * T) {
-    const int4 c_lo = *reinterpret_cast<const int4*>(cnt + d0);
-    const int4 c_hi = *reinterpret_cast<const int4*>(cnt + d0 + 4);
-    const int32_t c8[ND] = {c_lo.x, c_lo.y, c_lo.z, c_lo.w, c_hi.x, c_hi.y, c_hi.z, c_hi.w};
-    const uint2 kk = *reinterpret_cast<const uint2*>(kls + d0);
+  // 3. each document's first chunk within (range, class), and the copy-out
+  if (mine) {
+    const int32_t zero8[ND] = {0, 0, 0, 0, 0, 0, 0, 0};
     int32_t p8[ND];
+    uint32_t k_lo = 0, k_hi = 0;
 #pragma unroll
     for (int e = 0; e < ND; ++e) {
-      const int k = (int)(((e < 4 ? kk.x : kk.y) >> (8 * (e & 3))) & 0xFFu);
-      p8[e] = d0 + e < nd && c8[e] > 0
-                  ? atomicAdd(&cls[k], (c8[e] + kChunkPairs - 1) / kChunkPairs)
-                  : 0;
+      p8[e] = c8[e] > 0 ? atomicAdd(&cur[k8[e]], (c8[e] + kChunkPairs - 1) / kChunkPairs) : 0;
+      if (e < 4)
+        k_lo |= (uint32_t)k8[e] << (8 * e);
+      else
+        k_hi |= (uint32_t)k8[e] << (8 * (e - 4));
     }
-    store8_bounded(g.cnt, d0, nd, c8);
-    store8_bounded(g.dcur, d0, nd, zero8);
-    store8_bounded(g.cpos, d0, nd, p8);
+    store8_bounded(g.cnt, d0, d_hi, c8);
+    store8_bounded(g.dcur, d0, d_hi, zero8);
+    store8_bounded(g.cpos, d0, d_hi, p8);
+    if (d0 + 7 < d_hi) {
+      *reinterpret_cast<uint2*>(g.kls + d0) = uint2{k_lo, k_hi};
+    } else {
+#pragma unroll
+      for (int e = 0; e < ND; ++e)
+        if (d0 + e < d_hi) g.kls[d0 + e] = (uint8_t)k8[e];
+    }
   }
 }
 
 // scatter_docs_kernel (grid-stride, many workgroups): the chunk records.
-// Each pair takes the next place of its document (global cursors), i.e.
-// slot k % 4 of the document's chunk k / 4, and writes its id and its query
-// rows there (query length 0 when the pair or its document is invalid);
-// each document writes its rows into its chunks and marks the slots past its
-// last pair empty.  The order of a document's pairs follows the atomics; no
+// Each workgroup first turns the grouping's chunks per (range, class) into
+// the first chunk of each (range, class) -- classes in order (longest
+// documents first), ranges in order within a class -- in LDS.  Each pair
+// then takes the next place of its document (global cursors), i.e. slot
+// k % 4 of the document's chunk k / 4, and writes its id and its query rows
+// there (query length 0 when the pair or its document is invalid); each
+// document writes its rows into its chunks and marks the slots past its last
+// pair empty.  The order of a document's pairs follows the atomics; no
 // result depends on it.
-__global__ __launch_bounds__(256) void scatter_docs_kernel(FwdArgs a, DocChunks g) {
+constexpr int kScatterThreads = 256;
+static_assert(kScatterThreads == kLenClasses, "one thread per class in the prologue");
+__global__ __launch_bounds__(kScatterThreads) void scatter_docs_kernel(FwdArgs a, DocChunks g) {
+  __shared__ int32_t base[kGroupWgs][kLenClasses];
+  __shared__ int32_t wsum[kScatterThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  {
+    int h[kGroupWgs];
+#pragma unroll
+    for (int k = 0; k < kGroupWgs; ++k) h[k] = g.hist[k * kLenClasses + tid];
+    int tot = 0;
+#pragma unroll
+    for (int k = 0; k < kGroupWgs; ++k) {
+      base[k][tid] = tot;
+      tot += h[k];
+    }
+    // exclusive scan of the class totals over the workgroup
+    int inc = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(inc, o);
+      if (lane >= o) inc += u;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    int first = inc - tot;
+    for (int w = 0; w < wave; ++w) first += wsum[w];
+#pragma unroll
+    for (int k = 0; k < kGroupWgs; ++k) base[k][tid] += first;
+    if (blockIdx.x == 0 && tid == kScatterThreads - 1) g.nchunks[0] = first + tot;
+    __syncthreads();
+  }
   const int nd = (int)a.nd;
+  const int per = group_range(nd);
   const int64_t np = a.npairs;
   const int64_t n = np > nd ? np : nd;
+  auto first_chunk = [&](int d) __attribute__((always_inline)) {
+    return base[d / per][g.kls[d]] + g.cpos[d];
+  };
   auto doc_rows = [&](int64_t d, int& d0, int& ld) __attribute__((always_inline)) {
     const int64_t ds = a.doff[d], de = a.doff[d + 1];
     const bool ok = ds >= 0 && de > ds && de <= a.total_d;
     d0 = ok ? (int)ds : 0;
     ld = ok ? (int)(de - ds) : 0;
   };
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+  for (int64_t i = (int64_t)blockIdx.x * kScatterThreads + tid; i < n;
+       i += (int64_t)gridDim.x * kScatterThreads) {
     if (i < np) {
       const int32_t d = a.dids[i];
       if (d >= 0 && d < nd) {
         const int k = atomicAdd(&g.dcur[d], 1);
-        ChunkMeta& r = g.recs[g.cpos[d] + k / kChunkPairs];
+        ChunkMeta& r = g.recs[first_chunk(d) + k / kChunkPairs];
         const int j = k % kChunkPairs;
         int d0, ld;
         doc_rows(d, d0, ld);
@@ -1442,14 +1467,14 @@ __global__ __launch_bounds__(256) void scatter_docs_kernel(FwdArgs a, DocChunks 
       if (c > 0) {
         int d0, ld;
         doc_rows(i, d0, ld);
-        const int base = g.cpos[i];
+        const int fc = first_chunk((int)i);
         const int nch = (c + kChunkPairs - 1) / kChunkPairs;
         for (int jc = 0; jc < nch; ++jc) {
-          ChunkMeta& r = g.recs[base + jc];
+          ChunkMeta& r = g.recs[fc + jc];
           r.d_row0 = d0;
           r.ld = ld;
         }
-        ChunkMeta& last = g.recs[base + nch - 1];
+        ChunkMeta& last = g.recs[fc + nch - 1];
         for (int j = c - (nch - 1) * kChunkPairs; j < kChunkPairs; ++j) {
           last.p[j] = -1;
           last.q_row0[j] = 0;
@@ -1885,9 +1910,16 @@ static bool doc_chunk_fits(const FwdArgs& a, maxsim_dtype dtype, int max_lq) {
 }
 
 // Workspace: chunk records (64 bytes) [doc_chunk_bound], nchunks (int32,
-// padded to 16 bytes), then int32 cnt [nd], dcur [nd], cpos [nd].
+// padded to 16 bytes), int32 cnt [nd], dcur [nd], cpos [nd], hist
+// [kGroupWgs][kLenClasses] (16-byte aligned: 12 nd + 16 rounded up), then
+// the length classes (bytes) [nd].
+static size_t doc_chunk_hist_offset(int64_t nd, int64_t npairs) {
+  return (sizeof(ChunkMeta) * (size_t)doc_chunk_bound(nd, npairs) + 16 + 12 * (size_t)nd + 15) &
+         ~(size_t)15;
+}
 static size_t doc_chunk_ws_bytes(int64_t nd, int64_t npairs) {
-  return sizeof(ChunkMeta) * (size_t)doc_chunk_bound(nd, npairs) + 16 + 12 * (size_t)nd;
+  return doc_chunk_hist_offset(nd, npairs) + sizeof(int32_t) * kGroupWgs * kLenClasses +
+         (size_t)nd;
 }
 
 // Grid: as many workgroups as the chip holds at once (LDS or registers
@@ -1932,23 +1964,19 @@ static int run_doc_chunks(const FwdArgs& a, maxsim_dtype dtype, void* workspace,
   g.cnt = g.nchunks + 4;
   g.dcur = g.cnt + a.nd;
   g.cpos = g.dcur + a.nd;
-  // one workgroup counts and scans (5 bytes of LDS per document) ...
-  const size_t glds = (size_t)((a.nd + kGroupDocs - 1) / kGroupDocs * kGroupDocs) *
-                      (sizeof(int32_t) + 1);
+  g.hist = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
+                                      doc_chunk_hist_offset(a.nd, a.npairs));
+  g.kls = reinterpret_cast<uint8_t*>(g.hist + kGroupWgs * kLenClasses);
+  // the grouping workgroups count, classify and place by document range ...
   const bool vec = aligned16(a.dids) && aligned16(a.doff);
-  const auto gkern = vec ? group_docs_kernel<true> : group_docs_kernel<false>;
-  if (glds > 64 * 1024) {
-    // once per device, to what the largest grouping needs
-    static std::atomic<bool> raised[2][kMaxDevices];
-    if (int e = raise_lds_limit((const void*)gkern, (size_t)kDocGroupMaxDocs * (sizeof(int32_t) + 1),
-                                "group_docs_kernel", raised[vec]))
-      return e;
-  }
-  hipLaunchKernelGGL(gkern, dim3(1), dim3(kDocGroupThreads), glds, st, a, g);
+  hipLaunchKernelGGL(vec ? group_docs_kernel<true> : group_docs_kernel<false>, dim3(kGroupWgs),
+                     dim3(kDocGroupThreads), 0, st, a, g);
   // ... and the chip scatters the pair ids and the chunk table
   const int64_t n = std::max<int64_t>(a.npairs, a.nd);
-  const int64_t sgrid = std::min<int64_t>((n + 255) / 256, 4 * (int64_t)device_cus());
-  hipLaunchKernelGGL(scatter_docs_kernel, dim3((unsigned)sgrid), dim3(256), 0, st, a, g);
+  const int64_t sgrid =
+      std::min<int64_t>((n + kScatterThreads - 1) / kScatterThreads, 4 * (int64_t)device_cus());
+  hipLaunchKernelGGL(scatter_docs_kernel, dim3((unsigned)sgrid), dim3(kScatterThreads), 0, st, a,
+                     g);
   if (int e = check_launch("group_docs_kernel / scatter_docs_kernel")) return e;
   const int rc = dtype == MAXSIM_BFLOAT16 ? launch_doc_chunk<BF16>(a, g, bound, st)
                                           : launch_doc_chunk<F16>(a, g, bound, st);
