@@ -94,7 +94,8 @@ int maxsim_amd_packed_forward_with_argmax(
 /* Bytes of device workspace that let maxsim_amd_packed_forward_with_argmax_ws
  * score the pairs document by document: R + 16384 + num_documents, where R
  * is 64 * (ceil(num_pairs / 4) + min(num_documents, num_pairs)) + 16 +
- * 12 * num_documents rounded up to a multiple of 16.  No counterpart
+ * 8 * num_documents + 4 * num_pairs rounded up to a multiple of 16.  No
+ * counterpart
  * in the reference, whose packed forward scores the pairs in the caller's
  * order. */
 size_t maxsim_amd_packed_forward_workspace_size(int64_t num_documents, int64_t num_pairs);

@@ -1181,7 +1181,7 @@ struct DocChunks {
   ChunkMeta* recs;   // [max chunks], sorted by their document's length class
   int32_t* nchunks;  // [1]
   int32_t* cnt;      // [nd] pairs per document
-  int32_t* dcur;     // [nd] pairs of each document placed so far
+  int32_t* rank;     // [npairs] each pair's place among its document's pairs
   int32_t* cpos;     // [nd] each document's first chunk within (range, class)
   int32_t* hist;     // [kGroupWgs][kLenClasses] chunks per (range, class)
   uint8_t* kls;      // [nd] length class
@@ -1210,7 +1210,8 @@ __device__ __forceinline__ void write_unrouted_pair(const FwdArgs& a, int64_t p)
 
 // group_docs_kernel (kGroupWgs workgroups): workgroup k owns the documents
 // of range k.  It reads every pair id and counts the pairs of its range in
-// LDS counters, classifies its documents (length class, chunks per class),
+// LDS counters (the count before a pair is its place among its document's
+// pairs, written out for scatter_docs_kernel), classifies its documents (length class, chunks per class),
 // writes its chunks per class to hist[k], and gives each of its documents
 // a first chunk within (range, class) by LDS cursors.  scatter_docs_kernel
 // turns those into global positions (classes in order, ranges in order
@@ -1316,7 +1317,8 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
       for (int e = 0; e < 4; ++e) {
         const bool in = 4 * (v0 + (int64_t)u * T) + e < np;
         const int32_t d = di[u][e];
-        if (in && d >= d_lo && d < d_hi) atomicAdd(&cnt[d - d_lo], 1);
+        if (in && d >= d_lo && d < d_hi)
+          g.rank[4 * (v0 + (int64_t)u * T) + e] = atomicAdd(&cnt[d - d_lo], 1);
         bad |= in && (d < 0 || d >= nd);
       }
     if (writer && bad) {
@@ -1359,7 +1361,6 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
 
   // 3. each document's first chunk within (range, class), and the copy-out
   if (mine) {
-    const int32_t zero8[ND] = {0, 0, 0, 0, 0, 0, 0, 0};
     int32_t p8[ND];
     uint32_t k_lo = 0, k_hi = 0;
 #pragma unroll
@@ -1371,7 +1372,6 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
         k_hi |= (uint32_t)k8[e] << (8 * (e - 4));
     }
     store8_bounded(g.cnt, d0, d_hi, c8);
-    store8_bounded(g.dcur, d0, d_hi, zero8);
     store8_bounded(g.cpos, d0, d_hi, p8);
     if (d0 + 7 < d_hi) {
       *reinterpret_cast<uint2*>(g.kls + d0) = uint2{k_lo, k_hi};
@@ -1386,13 +1386,13 @@ __global__ __launch_bounds__(kDocGroupThreads) void group_docs_kernel(FwdArgs a,
 // scatter_docs_kernel (grid-stride, many workgroups): the chunk records.
 // Each workgroup first turns the grouping's chunks per (range, class) into
 // the first chunk of each (range, class) -- classes in order (longest
-// documents first), ranges in order within a class -- in LDS.  Each pair
-// then takes the next place of its document (global cursors), i.e. slot
-// k % 4 of the document's chunk k / 4, and writes its id and its query rows
+// documents first), ranges in order within a class -- in LDS.  Pair k of a
+// document (its place from the grouping) then takes slot k % 4 of the
+// document's chunk k / 4, and writes its id and its query rows
 // there (query length 0 when the pair or its document is invalid); each
 // document writes its rows into its chunks and marks the slots past its last
-// pair empty.  The order of a document's pairs follows the atomics; no
-// result depends on it.
+// pair empty.  The order of a document's pairs follows the grouping's
+// atomics; no result depends on it.
 constexpr int kScatterThreads = 256;
 static_assert(kScatterThreads == kLenClasses, "one thread per class in the prologue");
 __global__ __launch_bounds__(kScatterThreads) void scatter_docs_kernel(FwdArgs a, DocChunks g) {
@@ -1443,7 +1443,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_docs_kernel(FwdArgs a
     if (i < np) {
       const int32_t d = a.dids[i];
       if (d >= 0 && d < nd) {
-        const int k = atomicAdd(&g.dcur[d], 1);
+        const int k = g.rank[i];
         ChunkMeta& r = g.recs[first_chunk(d) + k / kChunkPairs];
         const int j = k % kChunkPairs;
         int d0, ld;
@@ -1910,11 +1910,12 @@ static bool doc_chunk_fits(const FwdArgs& a, maxsim_dtype dtype, int max_lq) {
 }
 
 // Workspace: chunk records (64 bytes) [doc_chunk_bound], nchunks (int32,
-// padded to 16 bytes), int32 cnt [nd], dcur [nd], cpos [nd], hist
-// [kGroupWgs][kLenClasses] (16-byte aligned: 12 nd + 16 rounded up), then
-// the length classes (bytes) [nd].
+// padded to 16 bytes), int32 cnt [nd], cpos [nd], rank [npairs], hist
+// [kGroupWgs][kLenClasses] (at a 16-byte boundary), then the length classes
+// (bytes) [nd].
 static size_t doc_chunk_hist_offset(int64_t nd, int64_t npairs) {
-  return (sizeof(ChunkMeta) * (size_t)doc_chunk_bound(nd, npairs) + 16 + 12 * (size_t)nd + 15) &
+  return (sizeof(ChunkMeta) * (size_t)doc_chunk_bound(nd, npairs) + 16 + 8 * (size_t)nd +
+          4 * (size_t)npairs + 15) &
          ~(size_t)15;
 }
 static size_t doc_chunk_ws_bytes(int64_t nd, int64_t npairs) {
@@ -1962,8 +1963,8 @@ static int run_doc_chunks(const FwdArgs& a, maxsim_dtype dtype, void* workspace,
   g.recs = static_cast<ChunkMeta*>(workspace);
   g.nchunks = reinterpret_cast<int32_t*>(g.recs + bound);
   g.cnt = g.nchunks + 4;
-  g.dcur = g.cnt + a.nd;
-  g.cpos = g.dcur + a.nd;
+  g.cpos = g.cnt + a.nd;
+  g.rank = g.cpos + a.nd;
   g.hist = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) +
                                       doc_chunk_hist_offset(a.nd, a.npairs));
   g.kls = reinterpret_cast<uint8_t*>(g.hist + kGroupWgs * kLenClasses);

@@ -80,13 +80,14 @@ def test_packed_forward_workspace_size(lib):
     fn.restype = ctypes.c_size_t
     fn.argtypes = [ctypes.c_int64, ctypes.c_int64]
     # 64-byte chunk records for ceil(P / 4) + min(nd, P) chunks, the chunk
-    # count (16 bytes), int32 per document (pairs, placed pairs, first chunk),
-    # to a 16-byte boundary; then 16 x 256 int32 chunk counts per (document
-    # range, length class) and one class byte per document
+    # count (16 bytes), int32 per document (pairs, first chunk) and per pair
+    # (place in its document), to a 16-byte boundary; then 16 x 256 int32
+    # chunk counts per (document range, length class) and one class byte per
+    # document
     def r16(x):
         return (x + 15) // 16 * 16
-    assert fn(8192, 20000) == r16(64 * (5000 + 8192) + 16 + 12 * 8192) + 16384 + 8192
-    assert fn(3, 4097) == r16(64 * (1025 + 3) + 16 + 12 * 3) + 16384 + 3
+    assert fn(8192, 20000) == r16(64 * (5000 + 8192) + 16 + 8 * 8192 + 4 * 20000) + 16384 + 8192
+    assert fn(3, 4097) == r16(64 * (1025 + 3) + 16 + 8 * 3 + 4 * 4097) + 16384 + 3
     assert fn(3, 4097) % 16 == 3 and fn(0, 0) == 16 + 16384
     assert fn(-1, 4) == 0 and fn(4, -1) == 0
 
