@@ -103,15 +103,32 @@ __device__ __forceinline__ void store8f(float* row, int k0, int dim, bool vec,
 // fp32 -> 16-bit gradient element, round to nearest even: torch's
 // float -> bfloat16 rule (NaN becomes the quiet NaN 0x7FC0) and the
 // hardware float -> half conversion under the default rounding mode, so a
-// gradient written here equals the fp32 gradient cast by torch.
+// gradient written here equals the fp32 gradient cast by torch.  For bf16
+// the hardware conversion (v_cvt_pk_bf16_f32 on gfx950) gives the rule's
+// bits for every non-NaN float (all 2^32 patterns compared on the device)
+// but keeps a NaN's sign and payload bits, so NaNs are replaced.
 template <typename O>
 __device__ __forceinline__ uint16_t to_out16(float f) {
   if constexpr (__is_same(O, BF16)) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)0x7fc0;
-    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    return f != f ? (uint16_t)0x7fc0 : __builtin_bit_cast(uint16_t, (__bf16)f);
   } else {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// Two 16-bit gradient elements in one word (a in the low half), bf16 in one
+// paired conversion.
+template <typename O>
+__device__ __forceinline__ uint32_t pack_out16(float a, float b) {
+  if constexpr (__is_same(O, BF16)) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    if (a != a) w = (w & 0xffff0000u) | 0x7fc0u;
+    if (b != b) w = (w & 0x0000ffffu) | 0x7fc00000u;
+    return w;
+  } else {
+    return (uint32_t)to_out16<O>(a) | ((uint32_t)to_out16<O>(b) << 16);
   }
 }
 
@@ -147,7 +164,7 @@ __device__ __forceinline__ void store8_nt(void* row_v, int k0, const float v[8])
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      w[e] = (uint32_t)to_out16<O>(v[2 * e]) | ((uint32_t)to_out16<O>(v[2 * e + 1]) << 16);
+      w[e] = pack_out16<O>(v[2 * e], v[2 * e + 1]);
     store16_nt(static_cast<uint16_t*>(row_v) + k0, u32x4_t{w[0], w[1], w[2], w[3]});
   }
 }
@@ -164,7 +181,7 @@ __device__ __forceinline__ void store8(void* row_v, int k0, int dim, bool vec, c
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        w[e] = (uint32_t)to_out16<O>(v[2 * e]) | ((uint32_t)to_out16<O>(v[2 * e + 1]) << 16);
+        w[e] = pack_out16<O>(v[2 * e], v[2 * e + 1]);
       *reinterpret_cast<uint4*>(row + k0) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
 #pragma unroll
@@ -755,8 +772,8 @@ __device__ __forceinline__ void dq_reduce_unit(const float* __restrict__ ws,
       reinterpret_cast<float4*>(dq)[x] = s;
     } else {
       reinterpret_cast<uint2*>(dq)[x] =
-          make_uint2((uint32_t)to_out16<O>(s.x) | ((uint32_t)to_out16<O>(s.y) << 16),
-                     (uint32_t)to_out16<O>(s.z) | ((uint32_t)to_out16<O>(s.w) << 16));
+          make_uint2(pack_out16<O>(s.x, s.y),
+                     pack_out16<O>(s.z, s.w));
     }
   } else {
     float s = ws[x];
@@ -1274,14 +1291,10 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[u][e] = 0.0f;
       void* dst = out_at<O>(a.dd, (d0 + r0 + rr) * (int64_t)a.dim);
-      const int s_end = start[rr + 1];
-      for (int s0 = start[rr]; s0 < s_end; s0 += kDdBlock) {
+      const int s_beg = start[rr], s_end = start[rr + 1];
+      // the fma sums of the entries [s0, s0 + kDdBlock) into sum
+      auto block = [&](int s0, float (&sum)[NS][8]) __attribute__((always_inline)) {
         const int s1 = min(s0 + kDdBlock, s_end);
-        float blk[NS][8];
-#pragma unroll
-        for (int u = 0; u < NS; ++u)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) blk[u][e] = 0.0f;
         // KB entries from s (KB = 8, or 4 for a short tail)
         auto batch = [&](int s, auto masked, auto kb) {
           constexpr bool MASKED = decltype(masked)::value;
@@ -1329,7 +1342,7 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
             for (int u = 0; u < NS; ++u)
 #pragma unroll
               for (int e = 0; e < 8; ++e)
-                blk[u][e] = fmaf(gx[k], frag_elem(f[k][u], e), blk[u][e]);
+                sum[u][e] = fmaf(gx[k], frag_elem(f[k][u], e), sum[u][e]);
         };
         using B8 = std::integral_constant<int, kBkBatch>;
         using B4 = std::integral_constant<int, kBkBatch / 2>;
@@ -1339,6 +1352,24 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
           batch(s, std::true_type{}, B8{});
         else if (s < s1)
           batch(s, std::true_type{}, B4{});
+      };
+      // The first block sums straight into the row sum; adding +0 then gives
+      // the bits of 0 + block (a chain from +0 ends at -0 only when a
+      // negative product rounds to zero, which this turns into +0).
+      if (s_beg < s_end) {
+        block(s_beg, acc);
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[u][e] += 0.0f;
+      }
+      for (int s0 = s_beg + kDdBlock; s0 < s_end; s0 += kDdBlock) {
+        float blk[NS][8];
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) blk[u][e] = 0.0f;
+        block(s0, blk);
 #pragma unroll
         for (int u = 0; u < NS; ++u)
 #pragma unroll
@@ -1508,7 +1539,7 @@ __device__ __forceinline__ void dd_padded_rows16(const PaddedDdArgs& a, int64_t 
         const int x = xs[2 * h];
         if (x < a.dim)
           *reinterpret_cast<uint32_t*>(row + x) =
-              (uint32_t)to_out16<O>(acc[2 * h]) | ((uint32_t)to_out16<O>(acc[2 * h + 1]) << 16);
+              pack_out16<O>(acc[2 * h], acc[2 * h + 1]);
       }
     } else {
 #pragma unroll
@@ -1601,10 +1632,10 @@ __device__ __forceinline__ void dd_padded_rows_vec(const PaddedDdArgs& a, int64_
         dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
       } else {
         uint4 o;
-        o.x = (uint32_t)to_out16<O>(acc[0]) | ((uint32_t)to_out16<O>(acc[1]) << 16);
-        o.y = (uint32_t)to_out16<O>(acc[2]) | ((uint32_t)to_out16<O>(acc[3]) << 16);
-        o.z = (uint32_t)to_out16<O>(acc[4]) | ((uint32_t)to_out16<O>(acc[5]) << 16);
-        o.w = (uint32_t)to_out16<O>(acc[6]) | ((uint32_t)to_out16<O>(acc[7]) << 16);
+        o.x = pack_out16<O>(acc[0], acc[1]);
+        o.y = pack_out16<O>(acc[2], acc[3]);
+        o.z = pack_out16<O>(acc[4], acc[5]);
+        o.w = pack_out16<O>(acc[6], acc[7]);
         *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.dd) + at) = o;
       }
     }
