@@ -216,6 +216,34 @@ def test_contrastive_backward_typed_equals_cast_fp32(Nq, Lq, dim, d_lens, dtype)
     assert_rounded_from(dd, dd32, mag)
 
 
+def test_contrastive_backward_typed_special_values_bits():
+    """16-bit gradients of score gradients with +NaN, -NaN, +-inf, signed
+    zeros and values whose products are fp32 denormals: the bits of the fp32
+    gradients cast by torch (every NaN becomes 0x7FC0, denormals round to
+    nearest even).  dq is summed in a fixed order; dd rows that receive one
+    entry have no order to differ in."""
+    q, d, off = make_contrastive(3, 8, 64, [40, 50, 33, 64, 100], torch.bfloat16, seed=41)
+    nan = float("nan")
+    dscore = torch.tensor([[nan, 0.5, -1e-39, 2.0, -0.0],
+                           [-1e-39, 3e-41, 1e-40, -7e-40, 2e-41],
+                           [1.0, -float("inf"), 0.0, -nan, 0.125]], device=DEVICE)
+    assert torch.signbit(dscore[2, 3])
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq32, dd32 = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    dq, dd = ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+    assert torch.isnan(dq32).any() and torch.isnan(dq).any()
+    assert (dq32.abs() < 1.1754944e-38).logical_and(dq32 != 0).any()   # fp32 denormals
+    assert torch.equal(dq.view(torch.int16), dq32.to(torch.bfloat16).view(torch.int16))
+    on, am = npi(off), npi(argmax)
+    hits = np.zeros(d.shape[0], dtype=np.int64)
+    for b in range(len(on) - 1):
+        np.add.at(hits, on[b] + am[:, b, :].reshape(-1), 1)
+    single = torch.from_numpy(hits == 1).to(DEVICE)
+    assert single.sum() >= 40
+    assert torch.equal(dd[single].view(torch.int16), dd32[single].to(torch.bfloat16).view(torch.int16))
+    assert torch.all(dd[torch.from_numpy(hits == 0).to(DEVICE)].view(torch.int16) == 0)
+
+
 def test_contrastive_backward_typed_single_pass_limit():
     """Through the C ABI: 16-bit gradients for Nq * (Lq + 1) = 19,800 entries
     (beyond an 80 KB LDS pass, within the 160 KB a workgroup may use) are
