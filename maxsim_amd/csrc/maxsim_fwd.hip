@@ -1,6 +1,6 @@
 // MaxSim forward kernels for gfx950 and the forward C-ABI entry points.
 //
-// Two kernels share the tile math of maxsim_common.h:
+// Three families of kernels share the tile math of maxsim_common.h:
 //
 //  * contrastive_tiled_kernel -- all-pairs scoring (reference K6/K7,
 //    maxsim.cu:1227-1595).  A workgroup of 8 waves holds up to 16 query
@@ -9,7 +9,15 @@
 //    global->LDS loads, so each document tile is read from L2 once per 16
 //    queries instead of once per pair.  The blockIdx -> (query group, doc
 //    chunk) map keeps all query groups of a doc chunk on one XCD so the
-//    chunk is fetched into that XCD's L2 once.
+//    chunk is fetched into that XCD's L2 once.  Chunks are runs of whole
+//    documents of equal work or, with few documents per chunk, documents
+//    dealt longest first so that every chunk holds the same tiles.
+//
+//  * group_docs_kernel + scatter_docs_kernel + doc_chunk_kernel -- packed
+//    pairs scored document by document (reference K9, maxsim.cu:1933-2108,
+//    with a workspace): the pairs are grouped by document on the device and
+//    each document's tiles pass once through an LDS ring shared by up to
+//    four of its pairs.
 //
 //  * pair_kernel -- one wave per run of (query, document) pairs, document
 //    rows loaded straight from global memory into MFMA operand registers
