@@ -363,6 +363,18 @@ def test_contrastive_dealt_chunks(nq, nb, lo, hi, n_long):
     assert torch.equal(maxsim_amd.score_contrastive(q, d, off), scores)
 
 
+@pytest.mark.parametrize("dim,dtype", [(32, torch.bfloat16), (64, torch.float32), (128, torch.float16)],
+                         ids=["d32-bf16", "d64-fp32", "d128-fp16"])
+def test_contrastive_dealt_chunks_other_shapes(dim, dtype):
+    """The dealt chunks at the other tile shapes the tiled kernel takes: the
+    ranking's scratch sits in the tile ring, smallest at dim 32 in bf16."""
+    gen = torch.Generator().manual_seed(dim)
+    lens = torch.randint(1, 900, (257,), generator=gen)
+    q, d, off = make_contrastive(64, 32, dim, lens.tolist(), dtype, seed=dim + 3, unit=True)
+    scores, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    _check_forward(q, d, off, scores, argmax)
+
+
 def test_contrastive_dealt_chunks_invalid_offsets_at_the_operator_level():
     """The dealt chunks with offsets that decrease at a few documents (called
     past the Python checks): those documents rank last (no tiles), get a NaN
