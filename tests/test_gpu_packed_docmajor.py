@@ -122,6 +122,28 @@ def test_doc_major_sparse_pairs(qlen, seed, shift):
     assert_close(s_doc[ok], s_ref, **SCORE_TOL[torch.bfloat16])
 
 
+@pytest.mark.parametrize("nd", [16384, 16381])
+def test_doc_major_at_the_document_cap(nd):
+    """The most documents the grouping takes (16 ranges of 1024) and a count
+    that leaves the last range ragged: the document-major path against
+    pair_kernel (max_q_len 65), bit for bit."""
+    gen = torch.Generator().manual_seed(nd)
+    nq, npairs, dim = 97, 40000, 64
+    ql = torch.randint(1, 65, (nq,), generator=gen)
+    dl = torch.randint(1, 40, (nd,), generator=gen)
+    q = torch.randn(int(ql.sum()), dim, generator=gen).to(torch.bfloat16).to(DEVICE)
+    d = torch.randn(int(dl.sum()), dim, generator=gen).to(torch.bfloat16).to(DEVICE)
+    qo, do = offsets_from_lengths(ql).to(DEVICE), offsets_from_lengths(dl).to(DEVICE)
+    qi = torch.randint(0, nq, (npairs,), generator=gen, dtype=torch.int32).to(DEVICE)
+    di = torch.randint(0, nd, (npairs,), generator=gen, dtype=torch.int32).to(DEVICE)
+    di[:3] = torch.tensor([nd - 1, nd - 1, 0], dtype=torch.int32)
+    s_doc, a_doc = ops.maxsim_packed_forward_with_argmax(q, qo, d, do, qi, di, 64)
+    s_pair, a_pair = ops.maxsim_packed_forward_with_argmax(q, qo, d, do, qi, di, 65)
+    torch.testing.assert_close(s_doc, s_pair, rtol=0, atol=0, equal_nan=True)
+    assert torch.equal(a_doc, a_pair[:, :64])
+    assert not torch.any(torch.isnan(s_doc))
+
+
 def test_c_abi_workspace_fallbacks():
     """Through the C ABI: a NULL, short or misaligned workspace takes the
     pair kernels; all three give the grouped path's bits."""
