@@ -1809,6 +1809,7 @@ __global__ __launch_bounds__(256) void pair_count_kernel(PackedBwdArgs a, Packed
 // group x) into group starts by an inclusive scan, workgroup 1 does dstart;
 // the cursors start at the group starts.
 constexpr int kScanThreads = 1024;
+constexpr int kScanPer = 16;  // values per thread held in registers (16,384 groups)
 __global__ __launch_bounds__(kScanThreads) void group_scan_kernel(PackedGroups g, int64_t nq,
                                                                   int64_t nd) {
   __shared__ int wave_tot[kScanThreads / 64];
@@ -1818,8 +1819,19 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_kernel(PackedGroups g
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t per = (n + kScanThreads - 1) / kScanThreads;
   const int64_t lo = min((int64_t)tid * per, n), hi = min(lo + per, n);
+  // a run of at most kScanPer values is loaded once, all loads in flight
+  // together (a loop of dependent round trips took most of the kernel)
+  int vals[kScanPer];
+  const bool short_run = per <= kScanPer;
   int run = 0;
-  for (int64_t x = lo; x < hi; ++x) run += v[x];
+  if (short_run) {
+#pragma unroll
+    for (int e = 0; e < kScanPer; ++e) vals[e] = lo + e < hi ? v[lo + e] : 0;
+#pragma unroll
+    for (int e = 0; e < kScanPer; ++e) run += vals[e];
+  } else {
+    for (int64_t x = lo; x < hi; ++x) run += v[x];
+  }
   int incl = run;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -1839,10 +1851,22 @@ __global__ __launch_bounds__(kScanThreads) void group_scan_kernel(PackedGroups g
   }
   __syncthreads();
   int acc = incl - run + (wave > 0 ? wave_tot[wave - 1] : 0);
-  for (int64_t x = lo; x < hi; ++x) {
-    acc += v[x];
-    v[x] = acc;
-    if (x < n - 1) cur[x] = acc;
+  if (short_run) {
+#pragma unroll
+    for (int e = 0; e < kScanPer; ++e) {
+      const int64_t x = lo + e;
+      if (x < hi) {
+        acc += vals[e];
+        v[x] = acc;
+        if (x < n - 1) cur[x] = acc;
+      }
+    }
+  } else {
+    for (int64_t x = lo; x < hi; ++x) {
+      acc += v[x];
+      v[x] = acc;
+      if (x < n - 1) cur[x] = acc;
+    }
   }
 }
 
@@ -1859,18 +1883,30 @@ __global__ __launch_bounds__(256) void pair_scatter_kernel(PackedBwdArgs a, Pack
 constexpr int kGroupThreads = 256;
 constexpr int kPairStage = 256;  // pairs staged in LDS at a time
 
-// Zero the rows [0, off[0]) and [off[nseg], total) of a [total, dim] output
-// of element type E (float or a 16-bit type): the rows before the first and
-// after the last segment, which no per-segment workgroup owns.
+// Before the grouped packed backward, one launch: zero the grouping's
+// counters (groups[0..n_groups)) and the rows of dq and dd before the first
+// and after the last segment, which no per-segment workgroup owns (element
+// type E: float, or 16-bit).  Against a fill and two zero_outside_kernel
+// launches, two launches fewer.
 template <typename E>
-__global__ __launch_bounds__(256) void zero_outside_kernel(E* out, const int32_t* off,
-                                                           int64_t nseg, int64_t total, int dim) {
-  const int64_t head = min(max((int64_t)off[0], (int64_t)0), total);
-  const int64_t tail = min(max((int64_t)off[nseg], head), total);
-  const int64_t n_head = head * dim, n_tail = (total - tail) * dim;
+__global__ __launch_bounds__(256) void packed_init_kernel(int32_t* groups, int64_t n_groups,
+                                                          E* dq, const int32_t* qoff, int64_t nq,
+                                                          int64_t total_q, E* dd,
+                                                          const int32_t* doff, int64_t nd,
+                                                          int64_t total_d, int dim) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n_head + n_tail; x += stride)
-    out[x < n_head ? x : tail * dim + (x - n_head)] = E(0);
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t x = t0; x < n_groups; x += stride) groups[x] = 0;
+  auto outside = [&](E* out, const int32_t* off, int64_t nseg, int64_t total) {
+    if (total <= 0) return;
+    const int64_t head = min(max((int64_t)off[0], (int64_t)0), total);
+    const int64_t tail = min(max((int64_t)off[nseg], head), total);
+    const int64_t n_head = head * dim, n_tail = (total - tail) * dim;
+    for (int64_t x = t0; x < n_head + n_tail; x += stride)
+      out[x < n_head ? x : tail * dim + (x - n_head)] = E(0);
+  };
+  outside(dq, qoff, nq, total_q);
+  outside(dd, doff, nd, total_d);
 }
 
 // dq: workgroup = (query qi, block of its tokens); thread = (token row,
@@ -2542,16 +2578,6 @@ static void launch_packed_grouped(const PackedBwdArgs& a, const PackedGroups& g,
   launch_packed_grouped_o<T, F32>(a, g, vec, G, st);
 }
 
-static void launch_zero_outside(void* out, bool out16, const int32_t* off, int64_t nseg,
-                                int64_t total, int64_t dim, hipStream_t st) {
-  if (out16)
-    hipLaunchKernelGGL(zero_outside_kernel<uint16_t>, dim3(64), dim3(256), 0, st,
-                       static_cast<uint16_t*>(out), off, nseg, total, (int)dim);
-  else
-    hipLaunchKernelGGL(zero_outside_kernel<float>, dim3(64), dim3(256), 0, st,
-                       static_cast<float*>(out), off, nseg, total, (int)dim);
-}
-
 template <typename T>
 static void launch_packed_bwd(const PackedBwdArgs& a, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((a.npairs + 3) / 4));
@@ -2696,20 +2722,27 @@ static int packed_backward_impl(
   g.dcur = g.dstart + (num_documents + 1);
   g.qlist = g.dcur + num_documents;
   g.dlist = g.qlist + num_pairs;
-  // zero qstart..dstart (qcur is written by the scan); fill works on the bits
-  launch_fill(reinterpret_cast<float*>(g.qstart),
-              (num_queries + 1) + num_queries + (num_documents + 1), st);
+  // zero qstart..dstart (qcur is written by the scan) and the gradient rows
+  // outside every segment
+  {
+    const int64_t ng = (num_queries + 1) + num_queries + (num_documents + 1);
+    if (out16)
+      hipLaunchKernelGGL(packed_init_kernel<uint16_t>, dim3(64), dim3(256), 0, st, g.qstart, ng,
+                         static_cast<uint16_t*>(dqueries), query_offsets, num_queries,
+                         total_q_tokens, static_cast<uint16_t*>(ddocuments), document_offsets,
+                         num_documents, total_d_tokens, (int)dim);
+    else
+      hipLaunchKernelGGL(packed_init_kernel<float>, dim3(64), dim3(256), 0, st, g.qstart, ng,
+                         static_cast<float*>(dqueries), query_offsets, num_queries,
+                         total_q_tokens, static_cast<float*>(ddocuments), document_offsets,
+                         num_documents, total_d_tokens, (int)dim);
+  }
   const int64_t pb = std::min<int64_t>((num_pairs + 255) / 256, 2048);
   hipLaunchKernelGGL(pair_count_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
   hipLaunchKernelGGL(group_scan_kernel, dim3(2), dim3(kScanThreads), 0, st, g, num_queries,
                      num_documents);
   hipLaunchKernelGGL(pair_scatter_kernel, dim3((unsigned)pb), dim3(256), 0, st, a, g);
   if (int e = check_launch("pair grouping kernels")) return e;
-  if (total_q_tokens > 0)
-    launch_zero_outside(dqueries, out16, query_offsets, num_queries, total_q_tokens, dim, st);
-  if (total_d_tokens > 0)
-    launch_zero_outside(ddocuments, out16, document_offsets, num_documents, total_d_tokens, dim,
-                        st);
   const int G = pow2_at_least(nslices < 16 ? nslices : 16);  // lanes per dd row
   const bool vec_g = vec && aligned16b(dqueries) && aligned16b(ddocuments);
   MAXSIM_DISPATCH(dtype, launch_packed_grouped, a, g, vec_g, G, out16, st);
