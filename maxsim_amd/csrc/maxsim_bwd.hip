@@ -838,6 +838,10 @@ struct DdArgs {
   int parts;             // dimension parts (1, 2, 4 or 8; divides kXcds)
   int part_slices;       // 8-element slices per part (last part may hold fewer)
   int group;             // lanes per row: power of two, <= 16, part_slices <= NS * group
+  // dd_bucket_kernel only: places per round of the deal (0: place b takes
+  // document b), and the shift that turns a document's rows into its key
+  int deal_places;
+  int deal_shift;
   // dd_bucket_kernel only: when dq_ws is set, each workgroup also adds its
   // share of the kXcds dQ partial sums once its document is done (the work
   // of dq_reduce_kernel, in the same order), so the memory-bound reduce
@@ -849,6 +853,8 @@ struct DdArgs {
 };
 
 constexpr int kDdThreads = 512;
+constexpr int kDdWaves = kDdThreads / 64;
+constexpr int kDealKeys = 64;  // document keys of the dD deal: rows >> deal_shift, clamped
 constexpr int kDdMaxGroup = 16;
 constexpr int kDdBatch = 8;      // bucket entries gathered per step
 constexpr int kDdBlock = 32;     // bucket entries per block sum
@@ -1131,9 +1137,10 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
   const int xcd = blockIdx.x % kXcds;
   const int per_part = kXcds / a.parts;
   const int part = xcd / per_part;
-  const int64_t b = (int64_t)(blockIdx.x / kXcds) * per_part + xcd % per_part;
-  if (b >= a.nb) return;
-  if (part == 0 && (b == 0 || b == a.nb - 1)) {
+  // place p of the grid (its workgroups: one per part)
+  const int64_t p = (int64_t)(blockIdx.x / kXcds) * per_part + xcd % per_part;
+  if (p >= a.nb) return;
+  if (part == 0 && (p == 0 || p == a.nb - 1)) {
     const int64_t head = min(max((int64_t)a.doff[0], (int64_t)0), a.total_d);
     const int64_t tail = min(max((int64_t)a.doff[a.nb], head), a.total_d);
     auto zero_rows = [&](int64_t lo, int64_t hi) {
@@ -1144,10 +1151,67 @@ __device__ __forceinline__ void dd_bucket_document(DdArgs a) {
           static_cast<uint16_t*>(a.dd)[x] = 0;
       }
     };
-    if (b == 0) zero_rows(0, head);
-    if (b == a.nb - 1) zero_rows(tail, a.total_d);
+    if (p == 0) zero_rows(0, head);
+    if (p == a.nb - 1) zero_rows(tail, a.total_d);
   }
-  const int64_t d0 = a.doff[b], d1 = a.doff[b + 1];
+  // The document of place p.  A workgroup's time follows its document's
+  // rows, and the workgroups of places p and p + deal_places run on one CU
+  // (workgroups w and w + CUs share a CU when the grid is dealt round-robin
+  // over the CUs) and share its VALU.  So the documents are ranked by rows,
+  // longest first (every workgroup ranks them all itself, one thread per
+  // document, the same ranks everywhere), and dealt so that the two places
+  // of a CU take ranks that add up to the same total: with n2 = nb - P
+  // places in the second round (P = deal_places), the P - n2 longest
+  // documents take the CUs with one place, and the others pair rank
+  // P - n2 + c with rank nb - 1 - c.  More than two rounds: longest first.
+  int64_t b = p, d0, d1;
+  if (a.deal_places > 0) {
+    // scratch from LDS byte 0 (the staged gradients and bucket arrays, not
+    // yet written); the pick in the last three ints of the cursor array,
+    // which the first pass writes two barriers after it is read
+    using Rank = RankScratch<kDdWaves, kDealKeys>;
+    const Rank rs(lds_i);
+    int* pick = ids - 3;                          // document, its first and end row
+    static_assert(Rank::kBytes <= (2 * (1024 + 1) - 3) * (int)sizeof(int),
+                  "ranking scratch ends before the pick");
+    rs.clear();
+    if (threadIdx.x == 0) pick[0] = -1;
+    const bool own = threadIdx.x < a.nb;
+    int key = 0, s0 = 0, e0 = 0;
+    if (own) {
+      s0 = a.doff[threadIdx.x];
+      e0 = a.doff[threadIdx.x + 1];
+      if (s0 >= 0 && e0 > s0 && (int64_t)e0 <= a.total_d)
+        key = min((e0 - s0) >> a.deal_shift, kDealKeys - 1);
+    }
+    const int r = rs.rank(own, key);
+    const int P = a.deal_places, nb = (int)a.nb, q = (int)p;
+    int want = q;  // a permutation of [0, nb) for any P
+    if (nb > P && nb <= 2 * P) {
+      const int n2 = nb - P;
+      want = q >= P ? nb - 1 - (q - P) : (q >= n2 ? q - n2 : P - n2 + q);
+    }
+    // the ranks are a permutation of [0, nb): exactly one thread matches
+    // (were none to, the place would keep its own document)
+    if (r == want) {
+      pick[0] = (int)threadIdx.x;
+      pick[1] = s0;
+      pick[2] = e0;
+    }
+    __syncthreads();
+    const int got = __builtin_amdgcn_readfirstlane(pick[0]);
+    if (got >= 0) {
+      b = got;
+      d0 = __builtin_amdgcn_readfirstlane(pick[1]);
+      d1 = __builtin_amdgcn_readfirstlane(pick[2]);
+    } else {
+      d0 = a.doff[b];
+      d1 = a.doff[b + 1];
+    }
+  } else {
+    d0 = a.doff[b];
+    d1 = a.doff[b + 1];
+  }
   if (d0 < 0 || d1 <= d0 || d1 > a.total_d) return;
   const int ld = (int)(d1 - d0);
   const int tid = threadIdx.x;
@@ -2872,6 +2936,24 @@ static int contrastive_backward_impl(
       ba.rows_per_pass = 1024;
       static_assert(kBkClasses + 1024 / 2 <= 1024 + 1, "row order does not fit the cursor array");
       ba.entries_per_pass = (int)ne_all;
+      // The deal, where a workgroup's time follows its document's rows: one
+      // part (a workgroup takes every slice of its document; with more parts
+      // it takes 1 / parts of the rows' work but buckets every entry), and
+      // two places per CU (P < nb <= 2 P, places b and b + P on one CU, P
+      // the CU count).  Keys are rows >> shift, with twice the mean length
+      // below kDealKeys.  Measured (typed backward, interleaved): C5 bf16
+      // 222.3 -> 217.3 us, 64-query shard 73.8 -> 68.0 us; the ranking
+      // alone costs about 2 us, and C2 (eight parts) lost 1.8 us with it.
+      const int cus = device_cus();
+      const int64_t places = cus;
+      if (parts == 1 && cus % kXcds == 0 && num_documents > places &&
+          num_documents <= 2 * places && num_documents <= kDdThreads) {
+        ba.deal_places = (int)places;
+        const int64_t twice_mean = 2 * total_d_tokens / num_documents;
+        int shift = 0;
+        while ((twice_mean >> shift) >= kDealKeys) ++shift;
+        ba.deal_shift = shift;
+      }
       blds = 2 * (size_t)(ba.rows_per_pass + 1) * sizeof(int) +
              ((size_t)ne_all + (size_t)num_queries) * sizeof(int);
       bucket = blds <= max_lds_per_block();

@@ -299,4 +299,78 @@ __device__ __forceinline__ void lds_dma16_nt(const void* base, uint32_t off, uin
       : "memory");
 }
 
+// ---------------------------------------------------------------------------
+// Ranking a workgroup's items (at most one per thread) by a small key,
+// largest key first, ties by thread index, so that every workgroup that
+// ranks the same keys finds the same ranks: the lists that are dealt to
+// workgroups longest first.  Each lane sets its bit in a 64-bit mask per
+// (wave, key) with one LDS atomic OR; its place among the lanes of equal
+// key is the count of bits below its own, the wave's count for the key the
+// count of all.  Wave 0 then turns the counts into the counts of the waves
+// before and each key's first rank (KEYS / 64 keys per lane).  No loop over
+// the distinct keys.
+// ---------------------------------------------------------------------------
+template <int kWaves, int KEYS>
+struct RankScratch {
+  static_assert(KEYS == 64 || KEYS == 128, "one or two keys per lane of wave 0");
+  static constexpr int kBytes = kWaves * KEYS * 8 + kWaves * KEYS * 4 + KEYS * 4;
+  uint64_t* mask;  // [wave][key] lanes holding the key
+  int* before;     // [wave][key] items of the key in the waves before
+  int* first;      // [key] first rank: items of the larger keys
+  __device__ explicit RankScratch(void* lds)
+      : mask(static_cast<uint64_t*>(lds)),
+        before(reinterpret_cast<int*>(mask + kWaves * KEYS)),
+        first(before + kWaves * KEYS) {}
+  // Clears the masks; every thread calls it, before rank().
+  __device__ void clear() const {
+    for (int i = threadIdx.x; i < kWaves * KEYS; i += kWaves * 64) mask[i] = 0;
+  }
+  // The rank of this thread's item (own: it has one; key in [0, KEYS)), or
+  // -1 without one.  Every thread of the workgroup calls it (three barriers,
+  // the first of which orders clear() before the atomics).
+  __device__ int rank(bool own, int key) const {
+    constexpr int KPL = KEYS / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (own) atomicOr(reinterpret_cast<unsigned long long*>(&mask[wave * KEYS + key]),
+                      1ull << lane);
+    __syncthreads();
+    int pos = 0;
+    if (own) pos = __popcll(mask[wave * KEYS + key] & ((1ull << lane) - 1ull));
+    if (wave == 0) {
+      int tot[KPL];
+      int sum = 0;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int k = KEYS - 1 - KPL * lane - j;
+        int cnt[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) cnt[w] = __popcll(mask[w * KEYS + k]);
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          before[w * KEYS + k] = t;
+          t += cnt[w];
+        }
+        tot[j] = t;
+        sum += t;
+      }
+      int ci = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(ci, o);
+        if (lane >= o) ci += u;
+      }
+      int run = ci - sum;
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        first[KEYS - 1 - KPL * lane - j] = run;
+        run += tot[j];
+      }
+    }
+    __syncthreads();
+    return own ? first[key] + before[wave * KEYS + key] + pos : -1;
+  }
+};
+
 }  // namespace maxsim

@@ -461,8 +461,8 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   //    to chunk p (r even) or n_dc - 1 - p (r odd), so every chunk gets a
   //    near-equal share of the tiles whatever the lengths.  Every workgroup
   //    ranks all documents itself (the same ranks everywhere): one thread
-  //    per document, ranks within a wave by ballot (a pass per distinct key
-  //    in the wave), counts per wave and key in LDS;
+  //    per document, RankScratch (a mask per wave and key set by LDS atomic
+  //    ORs, then a scan over the keys);
   //  * contiguous: the documents whose work prefix W(b) = off[b] + kDocWork
   //    * b falls in [dc, dc + 1) * W / n_dc, W = total_d + kDocWork * nb
   //    (rows, plus one tile's worth per document for its last partial tile
@@ -478,13 +478,15 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
   int n_docs = 0;
   if (a.n_dc > 1 && a.n_dc < a.nb && a.nb <= kTiledThreads &&
       a.nb < (int64_t)kDealtBelowDocsPerChunk * a.n_dc) {
-    // scratch in the tile ring, which no load has touched yet
-    static_assert((kTiledWaves + 1) * kLptKeys * (int)sizeof(int) <=
-                      kTileBuffers * G::kBufPieces * (int)sizeof(uint4),
-                  "ranking scratch fits the tile ring");
-    int* kcnt = reinterpret_cast<int*>(lds);       // [wave][key] counts, then waves-before
-    int* kfirst = kcnt + kTiledWaves * kLptKeys;   // [key] first rank
-    for (int i = tid; i < kTiledWaves * kLptKeys; i += kTiledThreads) kcnt[i] = 0;
+    // scratch in the tile ring, which no load has touched yet (half the
+    // keys where the ring is small: 32-element rows)
+    constexpr int kRing = kTileBuffers * G::kBufPieces * (int)sizeof(uint4);
+    constexpr int kKeys =
+        RankScratch<kTiledWaves, kLptKeys>::kBytes <= kRing ? kLptKeys : kLptKeys / 2;
+    using Rank = RankScratch<kTiledWaves, kKeys>;
+    static_assert(Rank::kBytes <= kRing, "ranking scratch fits the tile ring");
+    const Rank rs(lds);
+    rs.clear();
     const bool own = tid < a.nb;
     int s0 = 0, e0 = 0, key = 0;
     if (own) {
@@ -492,54 +494,11 @@ __global__ __launch_bounds__(kTiledThreads) void contrastive_tiled_kernel(TiledA
       e0 = a.doff[tid + 1];
       const bool ok = (s0 >= 0) && (e0 > s0) && ((int64_t)e0 <= a.total_d);
       const int t = ok ? (e0 - s0 + kTileRows - 1) / kTileRows : 0;
-      key = t < kLptKeys - 1 ? t : kLptKeys - 1;
+      key = t < kKeys - 1 ? t : kKeys - 1;
     }
-    __syncthreads();
-    // rank among the wave's lanes of equal key, and each key's count
-    uint64_t rem = __ballot(own);
-    int pos = 0;
-    while (rem) {
-      const int l0 = __ffsll((unsigned long long)rem) - 1;
-      const int k0 = __shfl(key, l0);
-      const uint64_t mk = __ballot(own && key == k0);
-      if (own && key == k0) pos = __popcll(mk & ((1ull << lane) - 1ull));
-      if (lane == l0) kcnt[wave * kLptKeys + k0] = __popcll(mk);
-      rem &= ~mk;
-    }
-    __syncthreads();
-    // per key (wave 0, two keys per lane, largest first): the counts of the
-    // waves before each wave, and the key's first rank, the total of the
-    // larger keys
-    static_assert(kLptKeys == 2 * 64, "two keys per lane of wave 0");
-    if (wave == 0) {
-      const int ka = kLptKeys - 1 - 2 * lane, kb = ka - 1;
-      int ca[kTiledWaves], cb[kTiledWaves];
-#pragma unroll
-      for (int w = 0; w < kTiledWaves; ++w) {
-        ca[w] = kcnt[w * kLptKeys + ka];
-        cb[w] = kcnt[w * kLptKeys + kb];
-      }
-      int ta = 0, tb = 0;
-#pragma unroll
-      for (int w = 0; w < kTiledWaves; ++w) {
-        kcnt[w * kLptKeys + ka] = ta;
-        kcnt[w * kLptKeys + kb] = tb;
-        ta += ca[w];
-        tb += cb[w];
-      }
-      int ci = ta + tb;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(ci, o);
-        if (lane >= o) ci += u;
-      }
-      kfirst[ka] = ci - ta - tb;
-      kfirst[kb] = ci - tb;
-    }
-    __syncthreads();
+    const int r = rs.rank(own, key);
     const int nc = a.n_dc, nbd = (int)a.nb;
     if (own) {
-      const int r = kfirst[key] + kcnt[wave * kLptKeys + key] + pos;
       const int rd = r / nc, p = r - rd * nc;
       if (((rd & 1) ? nc - 1 - p : p) == dc) {
         tab_s[rd] = s0;

@@ -511,3 +511,36 @@ def test_contrastive_backward_skewed_buckets(dtype):
         assert torch.equal(dqt, dq.to(dtype))
         _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
         assert_rounded_from(ddt, dd, mag)
+
+
+DEALT_DD = {
+    "ragged": lambda g: torch.randint(1, 401, (512,), generator=g).tolist(),
+    "equal-lengths": lambda g: [50] * 512,
+    "long-tail": lambda g: [5000 if i % 43 == 7 else 1 + i % 13 for i in range(512)],
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("lens", list(DEALT_DD), ids=list(DEALT_DD))
+def test_contrastive_backward_dealt_documents(lens, dtype):
+    """512 documents at dim 128 with 16-bit inputs: one dimension part and
+    two workgroups per CU on a 256-CU device, so the dD kernel ranks the
+    documents by rows and deals them (rank c and 511 - c to the workgroups
+    of one CU).  Ragged lengths, all lengths equal (every rank decided by
+    the document index) and a long tail past the largest key; fp32 and
+    typed gradients against the oracle."""
+    gen = torch.Generator().manual_seed(41)
+    d_lens = DEALT_DD[lens](gen)
+    Nq, Lq, dim = 8, 32, 128
+    q, d, off = make_contrastive(Nq, Lq, dim, d_lens, dtype, seed=43)
+    dscore = torch.randn(Nq, len(d_lens), generator=gen).to(DEVICE)
+    _, argmax = maxsim_amd.score_contrastive_with_argmax(q, d, off)
+    dq, dd = ops.maxsim_contrastive_backward(dscore, q, d, off, argmax)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q), np64(d), npi(off),
+                                                 npi(argmax))
+    assert_close(dq, dq_ref, **GRAD_TOL[dtype])
+    assert_close(dd, dd_ref, **GRAD_TOL[dtype])
+    dqt, ddt = ops.maxsim_contrastive_backward_typed(dscore, q, d, off, argmax)
+    assert torch.equal(dqt, dq.to(dtype))
+    _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
+    assert_rounded_from(ddt, dd, mag)
