@@ -2068,9 +2068,19 @@ __device__ __forceinline__ bool dd_packed_multi_stage(const PackedBwdArgs& a, in
   return a.slots > tc || n_pairs > min(kPairStage, kPkEntries / tc);
 }
 
+// Waves per SIMD the register allocation leaves room for.  With 16-bit rows
+// (half the write bytes) the kernel waits on each workgroup's chain of
+// dependent loads, and five workgroups per CU (96 VGPRs, a few spills in the
+// batch-of-8 path) beat four at 106 VGPRs: C4 typed backward 179.6 -> 170.3
+// us.  fp32 rows are bound by their writes, and the same bound cost 10 us
+// there (294.5 -> 304.6 us), so they keep the compiler's allocation, as do
+// unaligned rows (element loads: 148 VGPRs, whose cap would spill 47).
+template <bool VEC, int NS, typename O>
+constexpr int kPkMinWaves = (VEC && NS == 1 && O::bytes == 2) ? 5 : 1;
+
 template <typename T, bool VEC, int NS, typename O>
-__global__ __launch_bounds__(kGroupThreads) void dd_packed_kernel(PackedBwdArgs a,
-                                                                  PackedGroups g, int G) {
+__global__ __launch_bounds__(kGroupThreads, (kPkMinWaves<VEC, NS, O>)) void dd_packed_kernel(
+    PackedBwdArgs a, PackedGroups g, int G) {
   using S = typename T::storage;
   __shared__ int start[kPkRows + 1];
   __shared__ int cursor[kPkRows + 1];
