@@ -544,3 +544,53 @@ def test_contrastive_backward_dealt_documents(lens, dtype):
     assert torch.equal(dqt, dq.to(dtype))
     _, mag = ops.maxsim_contrastive_backward(dscore.abs(), q.abs(), d, off, argmax)
     assert_rounded_from(ddt, dd, mag)
+
+
+@pytest.mark.parametrize("grad_dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_contrastive_backward_dealt_documents_with_empty_ones_and_padding(grad_dtype):
+    """The dealt dD at 512 documents, called through the C ABI (no host
+    checks) into NaN-filled buffers: one document in ten is empty (its rank
+    is the lowest key's, its workgroup writes nothing), and rows before the
+    first and after the last document are padding.  Every row of every
+    document is written once -- a document dealt to no workgroup would keep
+    its NaNs -- and matches the oracle; padding rows are zero."""
+    import ctypes
+    from pathlib import Path
+
+    gen = torch.Generator().manual_seed(51)
+    lens = torch.randint(1, 121, (512,), generator=gen)
+    lens[torch.arange(512) % 10 == 3] = 0
+    nq, lq, dim = 8, 32, 128
+    pad_head, pad_tail = 3, 5
+    total = int(lens.sum())
+    q = torch.randn(nq, lq, dim, generator=gen).to(torch.bfloat16).to(DEVICE)
+    d = torch.randn(pad_head + total + pad_tail, dim, generator=gen).to(torch.bfloat16).to(DEVICE)
+    off_in = torch.zeros(513, dtype=torch.int32)
+    off_in[1:] = lens.cumsum(0)
+    off = (off_in + pad_head).to(DEVICE)
+    # argmax rows drawn inside each document (0 for the empty ones)
+    am = (torch.rand(nq, 512, lq, generator=gen) * lens.clamp(min=1)[None, :, None]).to(torch.int32)
+    am = am.to(DEVICE)
+    dscore = torch.randn(nq, 512, generator=gen).to(DEVICE)
+    n = d.shape[0]
+    dq = torch.full((nq, lq, dim), float("nan"), dtype=grad_dtype, device=DEVICE)
+    dd = torch.full((n, dim), float("nan"), dtype=grad_dtype, device=DEVICE)
+    lib = ctypes.CDLL(str(Path(maxsim_amd.__file__).resolve().parent / "libmaxsim_amd.so"))
+    I64, P = ctypes.c_int64, ctypes.c_void_p
+    fn = lib.maxsim_amd_contrastive_backward_typed
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, P, P, I64, I64, P, I64, P, I64, P, I64, P, P, P,
+                   ctypes.c_size_t, P]
+    BF16, F32 = 2, 0
+    rc = fn(BF16, F32 if grad_dtype == torch.float32 else BF16, dscore.data_ptr(), q.data_ptr(),
+            nq, lq, d.data_ptr(), n, off.data_ptr(), 512, am.data_ptr(), dim, dq.data_ptr(),
+            dd.data_ptr(), None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.all(dd[:pad_head] == 0) and torch.all(dd[n - pad_tail:] == 0)
+    dq_ref, dd_ref = oracle.contrastive_backward(np64(dscore), np64(q),
+                                                 np64(d[pad_head:n - pad_tail]), npi(off_in),
+                                                 npi(am))
+    body = dd[pad_head:n - pad_tail].float()
+    assert not torch.isnan(body).any()
+    assert_close(body, dd_ref, rtol=1e-2, atol=1e-3)
+    assert_close(dq.float(), dq_ref, rtol=1e-2, atol=1e-3)
