@@ -265,6 +265,105 @@ __global__ __launch_bounds__(256) void pair_kernel(FwdArgs a, int ppw) {
 }
 
 // ---------------------------------------------------------------------------
+// pair_split_kernel: batches with fewer pairs than the chip has SIMDs, where
+// pair_kernel's one wave per pair leaves most SIMDs idle (C1: 128 pairs of
+// ten fp32 tiles, each tile 64 MFMAs).  One workgroup of kSplitWaves waves
+// per pair: for each query block (one in registers), wave w scores tiles w,
+// w + kSplitWaves, ... in order, and the waves' per-token maxima are merged
+// in LDS (the larger value; on equal values the lower row).  Every tile gets
+// the same MFMAs and epilogue as in pair_kernel, and a wave's tiles come in
+// row order, so values, indices and the score sums (same order) are
+// bit-identical to pair_kernel's.
+// ---------------------------------------------------------------------------
+constexpr int kSplitWaves = 4;
+
+template <typename T, int KS, bool ARGMAX, bool VEC>
+__global__ __launch_bounds__(kSplitWaves * 64) void pair_split_kernel(FwdArgs a) {
+  using S = typename T::storage;
+  __shared__ float sm[kSplitWaves][kTileCols];
+  __shared__ int sa[kSplitWaves][kTileCols];
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t p = blockIdx.x;
+  if (p >= a.npairs) return;
+  const Pair pr = resolve_pair(a, p);
+  if (!pr.ok) {
+    if (w == 0) write_invalid_pair(a, p, lane);
+    return;
+  }
+  const S* __restrict__ Q = static_cast<const S*>(a.q);
+  const S* __restrict__ D = static_cast<const S*>(a.d);
+  const int dim = a.dim;
+  const int nblk = (pr.lq + kTileCols - 1) / kTileCols;
+  const int ntiles = (pr.ld + kTileRows - 1) / kTileRows;
+  auto load_tile = [&](int t, Frag<T> (&f)[KS]) __attribute__((always_inline)) {
+    const int r = min(t * kTileRows + c, pr.ld - 1);
+    const S* row = D + (pr.d_row0 + r) * (int64_t)dim;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) f[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, VEC);
+  };
+  float score = 0.0f;
+  for (int blk = 0; blk < nblk; ++blk) {
+    Frag<T> qf[KS];
+    {
+      const int tok = min(blk * kTileCols + c, pr.lq - 1);
+      const S* row = Q + (pr.q_row0 + tok) * (int64_t)dim;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[s] = load_frag<T>(row, kChunk * s + 8 * h, dim, VEC);
+    }
+    float m = -__builtin_inff();
+    int am = 0;
+    // this wave's tiles, the next one's fragments loading while one is scored
+    Frag<T> df[KS];
+    if (w < ntiles) load_tile(w, df);
+    for (int t = w; t < ntiles; t += kSplitWaves) {
+      Frag<T> nf[KS];
+      const bool more = t + kSplitWaves < ntiles;
+      if (more) load_tile(t + kSplitWaves, nf);
+      f32x16 acc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) mma_chunk(df[s], qf[s], acc);
+      tile_update<ARGMAX>(acc, m, am, t * kTileRows + 4 * h);
+      if (more) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) df[s] = nf[s];
+      }
+    }
+    merge_halves(m, am);
+    if (h == 0) {
+      sm[w][c] = m;
+      sa[w][c] = am;
+    }
+    __syncthreads();
+    if (w == 0) {
+      m = sm[0][c];
+      am = sa[0][c];
+#pragma unroll
+      for (int v = 1; v < kSplitWaves; ++v) {
+        const float mv = sm[v][c];
+        const int av = sa[v][c];
+        const bool wins = mv > m || (mv == m && av < am);
+        m = wins ? mv : m;
+        am = wins ? av : am;
+      }
+      const int tok = blk * kTileCols + c;
+      const bool valid = tok < pr.lq;
+      score += half_sum(valid ? m : 0.0f);
+      if (ARGMAX && h == 0 && tok < a.slots) a.argmax[p * a.slots + tok] = valid ? am : 0;
+    }
+    __syncthreads();  // the LDS slots are written again for the next block
+  }
+  if (w == 0) {
+    if (ARGMAX) {
+      for (int t = nblk * kTileCols + lane; t < a.slots; t += 64) a.argmax[p * a.slots + t] = 0;
+    }
+    if (lane == kHalfSumLane) a.scores[p] = score;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // wide_pair_kernel: embedding dims above kMaxRegDim, where a query block no
 // longer fits in registers.  One wave per pair; each 32x32 tile accumulates
 // over all K-chunks with both operands loaded per chunk (the query block is
@@ -1804,6 +1903,30 @@ static void launch_pair(const FwdArgs& a, int max_lq, int ppw, bool vec,
   }
 }
 
+template <typename T, int KS>
+static void launch_split_ks(const FwdArgs& a, bool vec, hipStream_t st) {
+  const dim3 grid((unsigned)a.npairs);
+  const dim3 block(kSplitWaves * 64);
+  if (a.argmax && vec)
+    hipLaunchKernelGGL((pair_split_kernel<T, KS, true, true>), grid, block, 0, st, a);
+  else if (a.argmax)
+    hipLaunchKernelGGL((pair_split_kernel<T, KS, true, false>), grid, block, 0, st, a);
+  else if (vec)
+    hipLaunchKernelGGL((pair_split_kernel<T, KS, false, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((pair_split_kernel<T, KS, false, false>), grid, block, 0, st, a);
+}
+
+template <typename T>
+static void launch_split(const FwdArgs& a, bool vec, hipStream_t st) {
+  switch (ks_for_dim(a.dim)) {
+    case 2: launch_split_ks<T, 2>(a, vec, st); break;
+    case 4: launch_split_ks<T, 4>(a, vec, st); break;
+    case 8: launch_split_ks<T, 8>(a, vec, st); break;
+    default: launch_split_ks<T, 16>(a, vec, st); break;
+  }
+}
+
 static int pairs_per_wave(int64_t npairs) {
   // Aim for ~16k waves (64 per CU, several rounds of the 8 resident per CU
   // at the two-block kernel's register use) so the last round is a small
@@ -1969,6 +2092,16 @@ static int run_pair(const FwdArgs& a, maxsim_dtype dtype, int max_lq,
   const int ppw = pairs_per_wave(a.npairs);
   const bool vec = (a.dim == ks_for_dim(a.dim) * kChunk) && aligned16(a.q) &&
                    aligned16(a.d);
+  // Fewer pairs than SIMDs: a workgroup per pair, its tiles split over the
+  // workgroup's waves (the same bits as pair_kernel).
+  if (a.npairs < (int64_t)4 * device_cus()) {
+    switch (dtype) {
+      case MAXSIM_BFLOAT16: launch_split<BF16>(a, vec, st); break;
+      case MAXSIM_FLOAT16: launch_split<F16>(a, vec, st); break;
+      default: launch_split<F32>(a, vec, st); break;
+    }
+    return check_launch("pair_split_kernel");
+  }
   // 16-bit rows of at most 128 elements, queries of at most two blocks:
   // the LDS-ring variant (two tiles in flight per wave)
   if (dtype != MAXSIM_FLOAT32 && vec && ks_for_dim(a.dim) <= 8 && max_lq <= 2 * kTileCols &&

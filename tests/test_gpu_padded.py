@@ -335,3 +335,37 @@ def test_padded_backward_row_paths_agree_bit_for_bit(Lq, dim, dtype):
         dq_b, dd_b = op(g, q_off, *rest)
         assert torch.equal(_bits(dq_a), _bits(dq_b))
         assert torch.equal(_bits(dd_a), _bits(dd_b))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_padded_small_batch_split_kernel_bits(dtype):
+    """Below one pair per SIMD the forward spreads each pair's tiles over the
+    waves of a workgroup and merges their maxima; from one pair per SIMD on,
+    a wave walks a pair's tiles in order.  The first 8 queries of a 64-query
+    batch (1024 pairs) and the same 8 queries alone (128 pairs) get the same
+    score and argmax bits, ties, NaN rows and -inf rows included, and match
+    the oracle."""
+    gen = torch.Generator().manual_seed(61)
+    B, C, Lq, Ld, dim = 64, 16, 40, 300, 128
+    q = torch.randn(B, Lq, dim, generator=gen).to(dtype)
+    d = torch.randn(B, C, Ld, dim, generator=gen).to(dtype)
+    d[0, 1, 7] = d[0, 1, 200]          # an exact tie across tiles
+    d[0, 2, 40] = float("nan")         # a NaN row never wins
+    d[1, 3, :] = float("-inf")         # every similarity -inf or NaN
+    qlen = torch.randint(1, Lq + 1, (B,), generator=gen, dtype=torch.int32)
+    dlen = torch.randint(1, Ld + 1, (B, C), generator=gen, dtype=torch.int32)
+    dlen[0, 1] = Ld
+    q, d, qlen, dlen = q.to(DEVICE), d.to(DEVICE), qlen.to(DEVICE), dlen.to(DEVICE)
+    s_all, a_all = maxsim_amd.score_candidates_padded_with_argmax(q, d, qlen, dlen)
+    s8, a8 = maxsim_amd.score_candidates_padded_with_argmax(q[:8].contiguous(), d[:8].contiguous(),
+                                                            qlen[:8].contiguous(),
+                                                            dlen[:8].contiguous())
+    torch.cuda.synchronize()
+    same = (s8.view(torch.int32) == s_all[:8].view(torch.int32))
+    assert bool(same.all())
+    assert torch.equal(a8, a_all[:8])
+    with np.errstate(invalid="ignore"):  # the -inf row's products are NaN
+        s_ref, a_ref = oracle.padded_forward(np64(q[:8]), np64(d[:8]), npi(qlen[:8]),
+                                             npi(dlen[:8]))
+    finite = np.isfinite(s_ref)
+    assert_close(s8[torch.as_tensor(finite, device=DEVICE)], s_ref[finite], **SCORE_TOL[dtype])
